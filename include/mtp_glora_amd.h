@@ -1,0 +1,145 @@
+/*
+ * mtp_glora_amd.h - C ABI of the MI355X (gfx950) streaming-KV-cache and
+ * MTP block-masked attention library (libmtp_glora_amd.so).
+ *
+ * Every entry point takes plain device pointers, element strides and sizes,
+ * enqueues its kernels on `stream` (a hipStream_t, NULL = default stream) and
+ * returns MGA_OK or an error code; mga_last_error() gives the message of the
+ * last failure on the calling thread. Nothing here allocates device memory:
+ * callers own every buffer (outputs and workspaces included).
+ *
+ * Layout conventions (batch size 1, as the reference assumes everywhere,
+ * mtp_glora/data_utils/collator.py:123-124, 242-243, 308-309):
+ *   - a [heads, seq, head_dim] operand is addressed as
+ *       base + h * stride_h + s * stride_s + d     (elements; d contiguous)
+ *   - dtype codes: MGA_DTYPE_BF16 or MGA_DTYPE_F32 (the model dtype);
+ *     attention arithmetic is bf16 MFMA with fp32 accumulation in both cases.
+ *   - the MTP mask is carried by one int32 code per chunk token:
+ *       -1 pad, -2 regular token (x), >= 0 mask token (m) = its
+ *       num_prefix_x value; every cached prefix key counts as x.
+ *   - block-mask tensors are the eight int32 arrays of a torch BlockMask with
+ *     B = H = 1 and 128 x 128 tiles: kv_num[nQ], kv_idx[nQ * nKV] (partial
+ *     tiles), full_kv_num / full_kv_idx (full tiles) and the q-major
+ *     transposes q_num[nKV], q_idx[nKV * nQ], full_q_num / full_q_idx.
+ */
+#ifndef MTP_GLORA_AMD_H
+#define MTP_GLORA_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MGA_OK 0
+#define MGA_ERR_INVALID 1   /* bad argument (shape, stride, alignment, dtype) */
+#define MGA_ERR_CAPACITY 2  /* cache capacity exceeded */
+#define MGA_ERR_HIP 3       /* HIP launch / runtime error */
+
+#define MGA_DTYPE_BF16 0
+#define MGA_DTYPE_F32 1
+
+#define MGA_BLOCK 128       /* BlockMask tile edge, [torch]nn/attention/flex_attention.py:395 */
+
+/* Library version (major * 10000 + minor * 100 + patch). */
+int mga_version(void);
+
+/* Message of the last error raised on the calling thread ("" if none). */
+const char *mga_last_error(void);
+
+/*
+ * Row copy into the preallocated cache:
+ *   dst[h, dst_offset + r, :] = src[h, idx ? idx[r] : r, :]   for r < n_rows, h < n_heads
+ * for K and V together.
+ * Replaces, with idx == NULL, the torch.cat of DynamicLayer.update
+ * ([tf]cache_utils.py:144-146; called at mtp_glora/models/modeling_qwen3.py:284
+ * and modeling_llama.py:317), and, with idx = the chunk's regular-token
+ * indices, the split + gather + cat + detach of
+ * mtp_glora/data_utils/collator.py:273-282.
+ * Errors: MGA_ERR_CAPACITY when dst_offset + n_rows > dst_capacity.
+ */
+int mga_kv_append(const void *src_k, const void *src_v, int64_t src_stride_h, int64_t src_stride_s,
+                  const int32_t *idx, int32_t n_rows,
+                  void *dst_k, void *dst_v, int64_t dst_stride_h, int64_t dst_stride_s,
+                  int64_t dst_offset, int64_t dst_capacity,
+                  int32_t n_heads, int32_t head_dim, int32_t dtype, void *stream);
+
+/*
+ * Indices of the regular tokens of a chunk: idx[0..count) = positions r with
+ * regular_mask[r * stride] != 0, ascending; *count written on the device.
+ * Replaces chunk['regular_token_mask'][0].nonzero() (collator.py:249).
+ */
+int mga_regular_index(const int64_t *regular_mask, int64_t stride, int32_t n,
+                      int32_t *idx, int32_t *count, void *stream);
+
+/*
+ * MTP block mask of a chunk with S tokens against a P-token cached prefix:
+ * writes the per-token codes and the eight BlockMask tensors that
+ * create_block_mask(mask_mod, B=None, H=None, Q_LEN=S, KV_LEN=P+S) returns for
+ * the mask_mod of collator.py:311-355 (collator.py:290-363), with
+ * nQ = ceil(S / 128), nKV = ceil((P + S) / 128).
+ * gate: the chunk's gate_mask (int64, -1 pad / 0 / 1), element stride gate_stride.
+ * tile_class: workspace of nQ * nKV bytes.
+ */
+int mga_mtp_block_mask(const int64_t *gate, int64_t gate_stride, int32_t S, int64_t P,
+                       int32_t *code, int8_t *tile_class,
+                       int32_t *kv_num, int32_t *kv_idx, int32_t *full_kv_num, int32_t *full_kv_idx,
+                       int32_t *q_num, int32_t *q_idx, int32_t *full_q_num, int32_t *full_q_idx,
+                       void *stream);
+
+/*
+ * MTP block-masked GQA attention forward over L = P + S keys:
+ *   o[s, h, :] = softmax_j(scale * q[h, s] . k[h / G, j], allowed(s, j)) v[h / G, j]
+ *   lse[h * S + s] = natural-log logsumexp (-inf, with o = 0, for a fully masked row)
+ * q: [Hq, S, D]; k, v: [Hkv, L, D]; o: [Hq, S, D] addressed with (o_sh, o_ss)
+ * (o_sh = D, o_ss = Hq * D gives the [S, Hq, D] layout the attention wrapper returns).
+ * Tiles are visited from the block-mask lists: empty tiles are skipped, partial
+ * tiles evaluate the mask per element from `code`, full tiles do not.
+ * Replaces flex_attention_forward ([tf]integrations/flex_attention.py:262-368)
+ * -> flex_attention ([torch]nn/attention/flex_attention.py:1396) as called from
+ * modeling_qwen3.py:286-300 / modeling_llama.py:320-332.
+ */
+int mga_attn_fwd(const void *q, int64_t q_sh, int64_t q_ss,
+                 const void *k, int64_t k_sh, int64_t k_ss,
+                 const void *v, int64_t v_sh, int64_t v_ss,
+                 void *o, int64_t o_sh, int64_t o_ss,
+                 float *lse, const int32_t *code,
+                 const int32_t *kv_num, const int32_t *kv_idx,
+                 const int32_t *full_kv_num, const int32_t *full_kv_idx,
+                 int32_t S, int32_t L, int32_t P, int32_t Hq, int32_t Hkv,
+                 int32_t head_dim, int32_t dtype, float scale, void *stream);
+
+/*
+ * Backward of mga_attn_fwd with grad_lse = 0 (the decoder discards the LSE,
+ * modeling_qwen3.py:341):
+ *   dq [Hq, S, D] for every visited tile (cached prefix included);
+ *   dk, dv [Hkv, L - grad_start, D] for keys j >= grad_start only, summed over
+ *   the G query heads of each kv head. With grad_start = P the detached
+ *   prefix (collator.py:279-280) gets no gradient and costs no dK/dV work.
+ * delta: workspace of Hq * S floats (rowsum(o * dout)).
+ * Replaces flex_attention's backward ([torch]_higher_order_ops/flex_attention.py:826-990)
+ * followed by the cat-backward of DynamicLayer.update.
+ * dq, dk, dv are fully written (no accumulation into existing contents).
+ */
+int mga_attn_bwd(const void *q, int64_t q_sh, int64_t q_ss,
+                 const void *k, int64_t k_sh, int64_t k_ss,
+                 const void *v, int64_t v_sh, int64_t v_ss,
+                 const void *o, int64_t o_sh, int64_t o_ss,
+                 const void *dout, int64_t do_sh, int64_t do_ss,
+                 const float *lse, float *delta,
+                 void *dq, int64_t dq_sh, int64_t dq_ss,
+                 void *dk, int64_t dk_sh, int64_t dk_ss,
+                 void *dv, int64_t dv_sh, int64_t dv_ss,
+                 int32_t grad_start, const int32_t *code,
+                 const int32_t *kv_num, const int32_t *kv_idx,
+                 const int32_t *full_kv_num, const int32_t *full_kv_idx,
+                 const int32_t *q_num, const int32_t *q_idx,
+                 const int32_t *full_q_num, const int32_t *full_q_idx,
+                 int32_t S, int32_t L, int32_t P, int32_t Hq, int32_t Hkv,
+                 int32_t head_dim, int32_t dtype, float scale, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MTP_GLORA_AMD_H */

@@ -1,0 +1,596 @@
+// MTP block-masked GQA attention, forward and backward, for gfx950.
+//
+// Arithmetic: bf16 operands on v_mfma_f32_32x32x16_bf16, fp32 accumulation,
+// softmax in the log2 domain (exp2 of scale*log2(e)*q.k). Semantics follow the
+// dense definition of flex_attention ([torch]_higher_order_ops/flex_attention.py
+// :202-267 fwd, :826-990 bwd): masked scores are -inf, a fully masked row has
+// output 0 and LSE -inf and receives no gradient.
+//
+// MFMA fragment conventions used throughout (32x32x16, wave64, l32 = lane & 31,
+// hi = lane >> 5):
+//   A operand (32 x 16):  lane supplies row l32, 8 k-values selected by (hi, slot)
+//   B operand (16 x 32):  lane supplies column l32, 8 k-values selected by (hi, slot)
+//   C (32 x 32, 16 regs): lane holds column l32, rows 8*(r>>2) + 4*hi + (r&3)
+// A and B pair their k-values by (hi, slot), so any fixed assignment of logical
+// k indices to (hi, slot) used identically on both operands gives the same
+// product. That is what lets an accumulator (C layout) feed the next MFMA as a
+// B operand without a shuffle: regs 8u..8u+7 of a lane are the logical k indices
+// 16u + 8*(t>>2) + 4*hi + (t&3), t = 0..7, and the A operand is read from LDS in
+// the same order (two runs of 4 consecutive elements).
+//
+// Orientation: the forward and dQ passes compute S^T = K Q^T (keys x queries),
+// so each lane owns one query column and the row softmax statistics stay in
+// the lane (plus one exchange with the lane 32 away). The dK/dV pass computes
+// S = Q K^T (queries x keys), so each lane owns one key column of dK^T / dV^T.
+#include "mga_common.hpp"
+#include "mga_internal.hpp"
+
+namespace mga {
+
+constexpr float kNegInf = -__builtin_huge_valf();
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// ---------------------------------------------------------------------------
+// LDS staging helpers (rows of 8-element vectors; the transposed copy is
+// written 4 keys x 1 dim at a time from 4 row loads).
+// ---------------------------------------------------------------------------
+
+// dst[r * ROW + c] = src[min(r0 + r, rmax) * ss + c] for r < NR, c < HD
+template <int HD, int NR, int ROW, int NT, typename T>
+__device__ __forceinline__ void stage_rows(bf16_t *dst, const T *src, int64_t ss, int r0, int rmax) {
+  constexpr int V8 = HD / 8;
+#pragma unroll
+  for (int vi = threadIdx.x; vi < NR * V8; vi += NT) {
+    const int r = vi / V8, c = (vi % V8) * 8;
+    const int row = min(r0 + r, rmax);
+    const bf16x8 x = load8(src + (int64_t)row * ss + c);
+    *reinterpret_cast<i32x4 *>(dst + r * ROW + c) = __builtin_bit_cast(i32x4, x);
+  }
+}
+
+// dst[c * ROW + r] = src[min(r0 + r, rmax) * ss + c] for r < NR, c < HD
+template <int HD, int NR, int ROW, int NT, typename T>
+__device__ __forceinline__ void stage_rows_t(bf16_t *dst, const T *src, int64_t ss, int r0, int rmax) {
+  constexpr int V8 = HD / 8;
+#pragma unroll
+  for (int it = threadIdx.x; it < (NR / 4) * V8; it += NT) {
+    const int dg = it % V8, kg = it / V8;
+    bf16x8 rows[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int row = min(r0 + kg * 4 + j, rmax);
+      rows[j] = load8(src + (int64_t)row * ss + dg * 8);
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      bf16x4 col;
+      col[0] = rows[0][e]; col[1] = rows[1][e]; col[2] = rows[2][e]; col[3] = rows[3][e];
+      *reinterpret_cast<i32x2 *>(dst + (dg * 8 + e) * ROW + kg * 4) = __builtin_bit_cast(i32x2, col);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Forward. One workgroup = one 128-row query tile of one query head, two
+// waves of 64 rows each. K and V^T are staged through LDS 64 keys at a time.
+// ---------------------------------------------------------------------------
+template <int HD, typename T>
+__global__ __launch_bounds__(128) void attn_fwd_kernel(AttnArgs a) {
+  constexpr int BK = 64;
+  constexpr int KS = HD / 16;
+  constexpr int DB = HD / 32;
+  constexpr int KROW = HD + 8;
+  constexpr int VROW = BK + 4;
+  constexpr int NT = 128;
+  __shared__ __attribute__((aligned(16))) bf16_t sK[BK * KROW];
+  __shared__ __attribute__((aligned(16))) bf16_t sVt[HD * VROW];
+  __shared__ __attribute__((aligned(16))) int sKc[BK];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, hi = lane >> 5;
+  const int G = a.Hq / a.Hkv;
+  // logical order (kv head, query tile descending, head in group); consecutive
+  // logical indices share an XCD so the G heads of a group share its L2.
+  const int li = xcd_swizzle(blockIdx.x, a.nQ * a.Hq);
+  const int hh = li % G;
+  const int rest = li / G;
+  const int qt = a.nQ - 1 - rest % a.nQ;
+  const int g = rest / a.nQ;
+  const int h = g * G + hh;
+
+  const T *qp = reinterpret_cast<const T *>(a.q) + h * a.q_sh;
+  const T *kp = reinterpret_cast<const T *>(a.k) + g * a.k_sh;
+  const T *vp = reinterpret_cast<const T *>(a.v) + g * a.v_sh;
+
+  bf16x8 qf[2][KS];
+  int qrow[2], qcode[2];
+#pragma unroll
+  for (int nb = 0; nb < 2; ++nb) {
+    qrow[nb] = qt * kBlock + wave * 64 + nb * 32 + l32;
+    const int qr = min(qrow[nb], a.S - 1);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) qf[nb][ks] = load8(qp + (int64_t)qr * a.q_ss + ks * 16 + hi * 8);
+    qcode[nb] = qrow[nb] < a.S ? a.code[qrow[nb]] : kCodePad;
+  }
+
+  float m_run[2] = {kNegInf, kNegInf};
+  float l_run[2] = {0.f, 0.f};
+  f32x16 oacc[2][DB];
+#pragma unroll
+  for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+    for (int db = 0; db < DB; ++db) oacc[nb][db] = zero16();
+
+  const int npart = a.kv_num[qt];
+  const int ntot = npart + a.fkv_num[qt];
+  const int32_t *pidx = a.kv_idx + (int64_t)qt * a.nKV;
+  const int32_t *fidx = a.fkv_idx + (int64_t)qt * a.nKV;
+
+  for (int it = 0; it < ntot; ++it) {
+    const bool partial = it < npart;
+    const int kt = partial ? pidx[it] : fidx[it - npart];
+    for (int sub = 0; sub < kBlock / BK; ++sub) {
+      const int kbase = kt * kBlock + sub * BK;
+      if (kbase >= a.L) break;
+      __syncthreads();
+      stage_rows<HD, BK, KROW, NT>(sK, kp, a.k_ss, kbase, a.L - 1);
+      stage_rows_t<HD, BK, VROW, NT>(sVt, vp, a.v_ss, kbase, a.L - 1);
+      if (tid < BK) sKc[tid] = key_code(a.code, kbase + tid, a.P, a.L);
+      __syncthreads();
+
+      f32x16 sacc[2][2];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) sacc[kb][nb] = zero16();
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+          const bf16x8 af = lds_read8(sK + (kb * 32 + l32) * KROW + ks * 16 + hi * 8);
+#pragma unroll
+          for (int nb = 0; nb < 2; ++nb) sacc[kb][nb] = mfma32(af, qf[nb][ks], sacc[kb][nb]);
+        }
+      }
+
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) {
+        float mx = kNegInf;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int kl0 = kb * 32 + 8 * i + 4 * hi;
+            const i32x4 kc = *reinterpret_cast<const i32x4 *>(sKc + kl0);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              float s = sacc[kb][nb][4 * i + j] * a.scale_log2;
+              if (partial && !mtp_allowed(qrow[nb] + a.P, qcode[nb], kbase + kl0 + j, kc[j])) s = kNegInf;
+              sacc[kb][nb][4 * i + j] = s;
+              mx = fmaxf(mx, s);
+            }
+          }
+        }
+        mx = fmaxf(mx, xor32(mx));
+        const float m_new = fmaxf(m_run[nb], mx);
+        const float m_use = m_new == kNegInf ? 0.f : m_new;
+        const float alpha = fast_exp2(m_run[nb] - m_use);
+        float ps = 0.f;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const float p = fast_exp2(sacc[kb][nb][r] - m_use);
+            sacc[kb][nb][r] = p;
+            ps += p;
+          }
+        l_run[nb] = l_run[nb] * alpha + ps;
+        m_run[nb] = m_new;
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) oacc[nb][db][r] *= alpha;
+      }
+
+      bf16x8 pb[2][2][2];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            const f32x16 &s = sacc[kb][nb];
+            pb[kb][nb][u] = pack8(s[8 * u + 0], s[8 * u + 1], s[8 * u + 2], s[8 * u + 3],
+                                  s[8 * u + 4], s[8 * u + 5], s[8 * u + 6], s[8 * u + 7]);
+          }
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            const bf16_t *vr = sVt + (db * 32 + l32) * VROW + kb * 32 + 16 * u + 4 * hi;
+            const bf16x8 af = lds_read4x2(vr, vr + 8);
+#pragma unroll
+            for (int nb = 0; nb < 2; ++nb) oacc[nb][db] = mfma32(af, pb[kb][nb][u], oacc[nb][db]);
+          }
+    }
+  }
+
+  T *op = reinterpret_cast<T *>(const_cast<void *>(a.o)) + h * a.o_sh;
+#pragma unroll
+  for (int nb = 0; nb < 2; ++nb) {
+    const float lt = l_run[nb] + xor32(l_run[nb]);
+    const float inv = lt > 0.f ? 1.f / lt : 0.f;
+    if (qrow[nb] < a.S) {
+      if (hi == 0)
+        a.lse[(int64_t)h * a.S + qrow[nb]] = lt > 0.f ? (m_run[nb] + __log2f(lt)) * kLn2 : kNegInf;
+      T *orow = op + (int64_t)qrow[nb] * a.o_ss;
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const f32x16 &c = oacc[nb][db];
+          store4(orow + db * 32 + 8 * i + 4 * hi, c[4 * i] * inv, c[4 * i + 1] * inv,
+                 c[4 * i + 2] * inv, c[4 * i + 3] * inv);
+        }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Backward prologue: delta[h, s] = sum_d o[s, h, d] * dout[s, h, d] (fp32).
+// ---------------------------------------------------------------------------
+template <int HD, typename T>
+__global__ __launch_bounds__(256) void attn_bwd_delta_kernel(AttnArgs a) {
+  constexpr int TPR = HD / 8;           // threads per row
+  constexpr int RPB = 256 / TPR;        // rows per block
+  const int rr = blockIdx.x * RPB + threadIdx.x / TPR;
+  const int c = (threadIdx.x % TPR) * 8;
+  float acc = 0.f;
+  const int nrows = a.S * a.Hq;
+  if (rr < nrows) {
+    const int s = rr / a.Hq, h = rr % a.Hq;
+    const bf16x8 o = load8(reinterpret_cast<const T *>(a.o) + h * a.o_sh + (int64_t)s * a.o_ss + c);
+    const bf16x8 d = load8(reinterpret_cast<const T *>(a.dout) + h * a.do_sh + (int64_t)s * a.do_ss + c);
+    if constexpr (sizeof(T) == 2) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc += (float)o[e] * (float)d[e];
+    }
+  }
+  if constexpr (sizeof(T) == 4) {
+    // fp32 operands: accumulate from the original values, not the bf16 copies
+    if (rr < nrows) {
+      const int s = rr / a.Hq, h = rr % a.Hq;
+      const float *o = reinterpret_cast<const float *>(a.o) + h * a.o_sh + (int64_t)s * a.o_ss + c;
+      const float *d = reinterpret_cast<const float *>(a.dout) + h * a.do_sh + (int64_t)s * a.do_ss + c;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc += o[e] * d[e];
+    }
+  }
+#pragma unroll
+  for (int off = TPR / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+  if (rr < nrows && (threadIdx.x % TPR) == 0) {
+    const int s = rr / a.Hq, h = rr % a.Hq;
+    a.delta[(int64_t)h * a.S + s] = acc;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Backward dQ pass. Same workgroup shape as the forward; K, K^T and V are
+// staged 32 keys at a time. Per key block:
+//   S^T = K Q^T, dP^T = V dO^T, P^T = exp2(S^T*c - lse2), dS^T = P^T (dP^T - delta),
+//   dQ^T += K^T dS^T.
+// ---------------------------------------------------------------------------
+template <int HD, typename T>
+__global__ __launch_bounds__(128) void attn_bwd_dq_kernel(AttnArgs a) {
+  constexpr int BK = 32;
+  constexpr int KS = HD / 16;
+  constexpr int DB = HD / 32;
+  constexpr int KROW = HD + 8;
+  constexpr int TROW = BK + 4;
+  constexpr int NT = 128;
+  __shared__ __attribute__((aligned(16))) bf16_t sK[BK * KROW];
+  __shared__ __attribute__((aligned(16))) bf16_t sV[BK * KROW];
+  __shared__ __attribute__((aligned(16))) bf16_t sKt[HD * TROW];
+  __shared__ __attribute__((aligned(16))) int sKc[BK];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, hi = lane >> 5;
+  const int G = a.Hq / a.Hkv;
+  const int li = xcd_swizzle(blockIdx.x, a.nQ * a.Hq);
+  const int hh = li % G;
+  const int rest = li / G;
+  const int qt = a.nQ - 1 - rest % a.nQ;
+  const int g = rest / a.nQ;
+  const int h = g * G + hh;
+
+  const T *qp = reinterpret_cast<const T *>(a.q) + h * a.q_sh;
+  const T *dop = reinterpret_cast<const T *>(a.dout) + h * a.do_sh;
+  const T *kp = reinterpret_cast<const T *>(a.k) + g * a.k_sh;
+  const T *vp = reinterpret_cast<const T *>(a.v) + g * a.v_sh;
+
+  bf16x8 qf[2][KS], df[2][KS];
+  int qrow[2], qcode[2];
+  float lse2[2], del[2];
+#pragma unroll
+  for (int nb = 0; nb < 2; ++nb) {
+    qrow[nb] = qt * kBlock + wave * 64 + nb * 32 + l32;
+    const int qr = min(qrow[nb], a.S - 1);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      qf[nb][ks] = load8(qp + (int64_t)qr * a.q_ss + ks * 16 + hi * 8);
+      df[nb][ks] = load8(dop + (int64_t)qr * a.do_ss + ks * 16 + hi * 8);
+    }
+    const bool in = qrow[nb] < a.S;
+    qcode[nb] = in ? a.code[qrow[nb]] : kCodePad;
+    lse2[nb] = in ? a.lse[(int64_t)h * a.S + qrow[nb]] * kLog2e : 0.f;
+    del[nb] = in ? a.delta[(int64_t)h * a.S + qrow[nb]] : 0.f;
+  }
+
+  f32x16 dqacc[2][DB];
+#pragma unroll
+  for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+    for (int db = 0; db < DB; ++db) dqacc[nb][db] = zero16();
+
+  const int npart = a.kv_num[qt];
+  const int ntot = npart + a.fkv_num[qt];
+  const int32_t *pidx = a.kv_idx + (int64_t)qt * a.nKV;
+  const int32_t *fidx = a.fkv_idx + (int64_t)qt * a.nKV;
+
+  for (int it = 0; it < ntot; ++it) {
+    const bool partial = it < npart;
+    const int kt = partial ? pidx[it] : fidx[it - npart];
+    for (int sub = 0; sub < kBlock / BK; ++sub) {
+      const int kbase = kt * kBlock + sub * BK;
+      if (kbase >= a.L) break;
+      __syncthreads();
+      stage_rows<HD, BK, KROW, NT>(sK, kp, a.k_ss, kbase, a.L - 1);
+      stage_rows<HD, BK, KROW, NT>(sV, vp, a.v_ss, kbase, a.L - 1);
+      stage_rows_t<HD, BK, TROW, NT>(sKt, kp, a.k_ss, kbase, a.L - 1);
+      if (tid < BK) sKc[tid] = key_code(a.code, kbase + tid, a.P, a.L);
+      __syncthreads();
+
+      f32x16 sacc[2], dpacc[2];
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) { sacc[nb] = zero16(); dpacc[nb] = zero16(); }
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const bf16x8 ak = lds_read8(sK + l32 * KROW + ks * 16 + hi * 8);
+        const bf16x8 av = lds_read8(sV + l32 * KROW + ks * 16 + hi * 8);
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) {
+          sacc[nb] = mfma32(ak, qf[nb][ks], sacc[nb]);
+          dpacc[nb] = mfma32(av, df[nb][ks], dpacc[nb]);
+        }
+      }
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int kl0 = 8 * i + 4 * hi;
+          const i32x4 kc = *reinterpret_cast<const i32x4 *>(sKc + kl0);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int r = 4 * i + j;
+            float p = fast_exp2(sacc[nb][r] * a.scale_log2 - lse2[nb]);
+            if (partial && !mtp_allowed(qrow[nb] + a.P, qcode[nb], kbase + kl0 + j, kc[j])) p = 0.f;
+            dpacc[nb][r] = p * (dpacc[nb][r] - del[nb]);
+          }
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        bf16x8 dsb[2];
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) {
+          const f32x16 &d = dpacc[nb];
+          dsb[nb] = pack8(d[8 * u + 0], d[8 * u + 1], d[8 * u + 2], d[8 * u + 3], d[8 * u + 4],
+                          d[8 * u + 5], d[8 * u + 6], d[8 * u + 7]);
+        }
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+          const bf16_t *kr = sKt + (db * 32 + l32) * TROW + 16 * u + 4 * hi;
+          const bf16x8 af = lds_read4x2(kr, kr + 8);
+#pragma unroll
+          for (int nb = 0; nb < 2; ++nb) dqacc[nb][db] = mfma32(af, dsb[nb], dqacc[nb][db]);
+        }
+      }
+    }
+  }
+
+  T *dqp = reinterpret_cast<T *>(a.dq) + h * a.dq_sh;
+#pragma unroll
+  for (int nb = 0; nb < 2; ++nb) {
+    if (qrow[nb] < a.S) {
+      T *row = dqp + (int64_t)qrow[nb] * a.dq_ss;
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const f32x16 &c = dqacc[nb][db];
+          store4(row + db * 32 + 8 * i + 4 * hi, c[4 * i] * a.scale, c[4 * i + 1] * a.scale,
+                 c[4 * i + 2] * a.scale, c[4 * i + 3] * a.scale);
+        }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Backward dK/dV pass over the key tiles that receive gradient (keys >=
+// grad_start). One workgroup = one 128-key tile of one kv head, four waves of
+// 32 keys; the G query heads of the group are reduced inside the workgroup.
+// Per 64-row query block of one head (staged natural and transposed):
+//   S = Q K^T, dP = dO V^T, P = exp2(S*c - lse2), dS = P (dP - delta),
+//   dV^T += dO^T P,  dK^T += Q^T dS.
+// ---------------------------------------------------------------------------
+template <int HD, typename T>
+__global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a, int kt0, int nkt) {
+  constexpr int BQ = 64;
+  constexpr int KS = HD / 16;
+  constexpr int DB = HD / 32;
+  constexpr int KROW = HD + 8;
+  constexpr int TROW = BQ + 4;
+  constexpr int NT = 256;
+  __shared__ __attribute__((aligned(16))) bf16_t sQ[BQ * KROW];
+  __shared__ __attribute__((aligned(16))) bf16_t sD[BQ * KROW];
+  __shared__ __attribute__((aligned(16))) bf16_t sQt[HD * TROW];
+  __shared__ __attribute__((aligned(16))) bf16_t sDt[HD * TROW];
+  __shared__ __attribute__((aligned(16))) float sL[BQ];
+  __shared__ __attribute__((aligned(16))) float sDel[BQ];
+  __shared__ __attribute__((aligned(16))) int sC[BQ];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, hi = lane >> 5;
+  const int G = a.Hq / a.Hkv;
+  const int li = xcd_swizzle(blockIdx.x, nkt * a.Hkv);
+  const int g = li / nkt;
+  const int kt = kt0 + li % nkt;
+
+  const int key = kt * kBlock + wave * 32 + l32;
+  const int kr = min(key, a.L - 1);
+  const int kcode = key_code(a.code, key, a.P, a.L);
+  const T *kp = reinterpret_cast<const T *>(a.k) + g * a.k_sh + (int64_t)kr * a.k_ss;
+  const T *vp = reinterpret_cast<const T *>(a.v) + g * a.v_sh + (int64_t)kr * a.v_ss;
+  bf16x8 kf[KS], vf[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    kf[ks] = load8(kp + ks * 16 + hi * 8);
+    vf[ks] = load8(vp + ks * 16 + hi * 8);
+  }
+  f32x16 dkacc[DB], dvacc[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) { dkacc[db] = zero16(); dvacc[db] = zero16(); }
+
+  const int npart = a.q_num[kt];
+  const int ntot = npart + a.fq_num[kt];
+  const int32_t *pidx = a.q_idx + (int64_t)kt * a.nQ;
+  const int32_t *fidx = a.fq_idx + (int64_t)kt * a.nQ;
+
+  for (int it = 0; it < ntot; ++it) {
+    const bool partial = it < npart;
+    const int qt = partial ? pidx[it] : fidx[it - npart];
+    for (int hh = 0; hh < G; ++hh) {
+      const int h = g * G + hh;
+      const T *qp = reinterpret_cast<const T *>(a.q) + h * a.q_sh;
+      const T *dop = reinterpret_cast<const T *>(a.dout) + h * a.do_sh;
+      for (int sub = 0; sub < kBlock / BQ; ++sub) {
+        const int q0 = qt * kBlock + sub * BQ;
+        if (q0 >= a.S) break;
+        __syncthreads();
+        stage_rows<HD, BQ, KROW, NT>(sQ, qp, a.q_ss, q0, a.S - 1);
+        stage_rows<HD, BQ, KROW, NT>(sD, dop, a.do_ss, q0, a.S - 1);
+        stage_rows_t<HD, BQ, TROW, NT>(sQt, qp, a.q_ss, q0, a.S - 1);
+        stage_rows_t<HD, BQ, TROW, NT>(sDt, dop, a.do_ss, q0, a.S - 1);
+        if (tid < BQ) {
+          const int q = q0 + tid;
+          const bool in = q < a.S;
+          sL[tid] = in ? a.lse[(int64_t)h * a.S + q] * kLog2e : 0.f;
+          sDel[tid] = in ? a.delta[(int64_t)h * a.S + q] : 0.f;
+          sC[tid] = in ? a.code[q] : kCodePad;
+        }
+        __syncthreads();
+
+#pragma unroll
+        for (int qb = 0; qb < BQ / 32; ++qb) {
+          f32x16 sacc = zero16(), dpacc = zero16();
+#pragma unroll
+          for (int ks = 0; ks < KS; ++ks) {
+            const bf16x8 aq = lds_read8(sQ + (qb * 32 + l32) * KROW + ks * 16 + hi * 8);
+            const bf16x8 ad = lds_read8(sD + (qb * 32 + l32) * KROW + ks * 16 + hi * 8);
+            sacc = mfma32(aq, kf[ks], sacc);
+            dpacc = mfma32(ad, vf[ks], dpacc);
+          }
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int ql0 = qb * 32 + 8 * i + 4 * hi;
+            const f32x4 l4 = *reinterpret_cast<const f32x4 *>(sL + ql0);
+            const f32x4 d4 = *reinterpret_cast<const f32x4 *>(sDel + ql0);
+            const i32x4 c4 = *reinterpret_cast<const i32x4 *>(sC + ql0);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const int r = 4 * i + j;
+              float p = fast_exp2(sacc[r] * a.scale_log2 - l4[j]);
+              if (partial && !mtp_allowed(q0 + ql0 + j + a.P, c4[j], key, kcode)) p = 0.f;
+              sacc[r] = p;
+              dpacc[r] = p * (dpacc[r] - d4[j]);
+            }
+          }
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            const bf16x8 pb = pack8(sacc[8 * u + 0], sacc[8 * u + 1], sacc[8 * u + 2], sacc[8 * u + 3],
+                                    sacc[8 * u + 4], sacc[8 * u + 5], sacc[8 * u + 6], sacc[8 * u + 7]);
+            const bf16x8 dsb = pack8(dpacc[8 * u + 0], dpacc[8 * u + 1], dpacc[8 * u + 2],
+                                     dpacc[8 * u + 3], dpacc[8 * u + 4], dpacc[8 * u + 5],
+                                     dpacc[8 * u + 6], dpacc[8 * u + 7]);
+#pragma unroll
+            for (int db = 0; db < DB; ++db) {
+              const int off = (db * 32 + l32) * TROW + qb * 32 + 16 * u + 4 * hi;
+              const bf16x8 adt = lds_read4x2(sDt + off, sDt + off + 8);
+              const bf16x8 aqt = lds_read4x2(sQt + off, sQt + off + 8);
+              dvacc[db] = mfma32(adt, pb, dvacc[db]);
+              dkacc[db] = mfma32(aqt, dsb, dkacc[db]);
+            }
+          }
+        }
+      }
+    }
+  }
+
+  if (key >= a.grad_start && key < a.L) {
+    const int64_t row = key - a.grad_start;
+    T *dkr = reinterpret_cast<T *>(a.dk) + g * a.dk_sh + row * a.dk_ss;
+    T *dvr = reinterpret_cast<T *>(a.dv) + g * a.dv_sh + row * a.dv_ss;
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int d0 = db * 32 + 8 * i + 4 * hi;
+        const f32x16 &ck = dkacc[db];
+        const f32x16 &cv = dvacc[db];
+        store4(dkr + d0, ck[4 * i] * a.scale, ck[4 * i + 1] * a.scale, ck[4 * i + 2] * a.scale,
+               ck[4 * i + 3] * a.scale);
+        store4(dvr + d0, cv[4 * i], cv[4 * i + 1], cv[4 * i + 2], cv[4 * i + 3]);
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Launchers
+// ---------------------------------------------------------------------------
+template <int HD, typename T>
+static void fwd_impl(const AttnArgs &a, hipStream_t st) {
+  hipLaunchKernelGGL((attn_fwd_kernel<HD, T>), dim3(a.nQ * a.Hq), dim3(128), 0, st, a);
+}
+
+template <int HD, typename T>
+static void bwd_impl(const AttnArgs &a, hipStream_t st) {
+  constexpr int RPB = 256 / (HD / 8);
+  const int rows = a.S * a.Hq;
+  hipLaunchKernelGGL((attn_bwd_delta_kernel<HD, T>), dim3((rows + RPB - 1) / RPB), dim3(256), 0, st, a);
+  hipLaunchKernelGGL((attn_bwd_dq_kernel<HD, T>), dim3(a.nQ * a.Hq), dim3(128), 0, st, a);
+  const int kt0 = a.grad_start / kBlock;
+  const int nkt = a.nKV - kt0;
+  if (nkt > 0 && a.grad_start < a.L)
+    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<HD, T>), dim3(nkt * a.Hkv), dim3(256), 0, st, a, kt0, nkt);
+}
+
+void launch_attn_fwd(const AttnArgs &a, int head_dim, bool is_f32, hipStream_t st) {
+  if (head_dim == 128) {
+    if (is_f32) fwd_impl<128, float>(a, st); else fwd_impl<128, bf16_t>(a, st);
+  } else {
+    if (is_f32) fwd_impl<64, float>(a, st); else fwd_impl<64, bf16_t>(a, st);
+  }
+}
+
+void launch_attn_bwd(const AttnArgs &a, int head_dim, bool is_f32, hipStream_t st) {
+  if (head_dim == 128) {
+    if (is_f32) bwd_impl<128, float>(a, st); else bwd_impl<128, bf16_t>(a, st);
+  } else {
+    if (is_f32) bwd_impl<64, float>(a, st); else bwd_impl<64, bf16_t>(a, st);
+  }
+}
+
+}  // namespace mga

@@ -1,0 +1,199 @@
+// C ABI entry points (declared in include/mtp_glora_amd.h): argument checks,
+// then kernel launches on the caller's stream. No device allocation happens here.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "../../include/mtp_glora_amd.h"
+#include "mga_common.hpp"
+#include "mga_internal.hpp"
+
+namespace {
+
+thread_local char g_err[1024] = {0};
+
+int fail(int code, const char *fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int check_launch(const char *what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(MGA_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+  g_err[0] = 0;
+  return MGA_OK;
+}
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+int elem_bytes(int dtype) { return dtype == MGA_DTYPE_BF16 ? 2 : (dtype == MGA_DTYPE_F32 ? 4 : 0); }
+
+// A [heads, rows, head_dim] operand addressed with element strides: every row
+// start must be 16-byte aligned for the vector loads.
+int check_operand(const char *name, const void *p, int64_t sh, int64_t ss, int eb) {
+  if (!p) return fail(MGA_ERR_INVALID, "%s: null pointer", name);
+  if (!aligned16(p)) return fail(MGA_ERR_INVALID, "%s: base pointer not 16-byte aligned", name);
+  if (sh < 0 || ss <= 0) return fail(MGA_ERR_INVALID, "%s: invalid strides (%lld, %lld)", name,
+                                      (long long)sh, (long long)ss);
+  if (((sh * eb) & 15) || ((ss * eb) & 15))
+    return fail(MGA_ERR_INVALID, "%s: strides (%lld, %lld) elements are not multiples of 16 bytes",
+                name, (long long)sh, (long long)ss);
+  return MGA_OK;
+}
+
+int check_attn_common(int32_t S, int32_t L, int32_t P, int32_t Hq, int32_t Hkv, int32_t hd,
+                      int32_t dtype) {
+  if (S <= 0) return fail(MGA_ERR_INVALID, "S must be positive (got %d)", S);
+  if (P < 0 || L != P + S) return fail(MGA_ERR_INVALID, "need L == P + S (L=%d P=%d S=%d)", L, P, S);
+  if (Hq <= 0 || Hkv <= 0 || Hq % Hkv) return fail(MGA_ERR_INVALID, "Hq (%d) must be a positive multiple of Hkv (%d)", Hq, Hkv);
+  if (hd != 64 && hd != 128) return fail(MGA_ERR_INVALID, "head_dim must be 64 or 128 (got %d)", hd);
+  if (!elem_bytes(dtype)) return fail(MGA_ERR_INVALID, "unknown dtype code %d", dtype);
+  return MGA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mga_version(void) { return 100; }
+
+const char *mga_last_error(void) { return g_err; }
+
+int mga_kv_append(const void *src_k, const void *src_v, int64_t src_stride_h, int64_t src_stride_s,
+                  const int32_t *idx, int32_t n_rows, void *dst_k, void *dst_v,
+                  int64_t dst_stride_h, int64_t dst_stride_s, int64_t dst_offset,
+                  int64_t dst_capacity, int32_t n_heads, int32_t head_dim, int32_t dtype,
+                  void *stream) {
+  const int eb = elem_bytes(dtype);
+  if (!eb) return fail(MGA_ERR_INVALID, "mga_kv_append: unknown dtype code %d", dtype);
+  if (n_rows < 0 || n_heads <= 0 || head_dim <= 0)
+    return fail(MGA_ERR_INVALID, "mga_kv_append: bad sizes (rows=%d heads=%d head_dim=%d)", n_rows,
+                n_heads, head_dim);
+  const int row_bytes = head_dim * eb;
+  if (row_bytes < 16 || (row_bytes & (row_bytes - 1)))
+    return fail(MGA_ERR_INVALID, "mga_kv_append: head_dim*elem (%d bytes) must be a power of two >= 16",
+                row_bytes);
+  if (dst_offset < 0 || dst_offset + n_rows > dst_capacity)
+    return fail(MGA_ERR_CAPACITY, "mga_kv_append: rows [%lld, %lld) exceed the cache capacity %lld",
+                (long long)dst_offset, (long long)(dst_offset + n_rows), (long long)dst_capacity);
+  int rc;
+  if ((rc = check_operand("src_k", src_k, src_stride_h, src_stride_s, eb))) return rc;
+  if ((rc = check_operand("src_v", src_v, src_stride_h, src_stride_s, eb))) return rc;
+  if ((rc = check_operand("dst_k", dst_k, dst_stride_h, dst_stride_s, eb))) return rc;
+  if ((rc = check_operand("dst_v", dst_v, dst_stride_h, dst_stride_s, eb))) return rc;
+  if ((int64_t)n_rows * (row_bytes / 16) > 0x7fffffffLL)
+    return fail(MGA_ERR_INVALID, "mga_kv_append: too many rows per head (%d)", n_rows);
+  if (n_rows == 0) { g_err[0] = 0; return MGA_OK; }
+  mga::launch_kv_copy_rows(src_k, src_v, src_stride_h * eb, src_stride_s * eb, idx, n_rows, dst_k,
+                           dst_v, dst_stride_h * eb, dst_stride_s * eb, dst_offset, n_heads,
+                           row_bytes, (hipStream_t)stream);
+  return check_launch("mga_kv_append");
+}
+
+int mga_regular_index(const int64_t *regular_mask, int64_t stride, int32_t n, int32_t *idx,
+                      int32_t *count, void *stream) {
+  if (!regular_mask || !idx || !count) return fail(MGA_ERR_INVALID, "mga_regular_index: null pointer");
+  if (n <= 0 || stride <= 0) return fail(MGA_ERR_INVALID, "mga_regular_index: bad size/stride (%d, %lld)", n, (long long)stride);
+  mga::launch_regular_index(regular_mask, stride, n, idx, count, (hipStream_t)stream);
+  return check_launch("mga_regular_index");
+}
+
+int mga_mtp_block_mask(const int64_t *gate, int64_t gate_stride, int32_t S, int64_t P,
+                       int32_t *code, int8_t *tile_class, int32_t *kv_num, int32_t *kv_idx,
+                       int32_t *full_kv_num, int32_t *full_kv_idx, int32_t *q_num, int32_t *q_idx,
+                       int32_t *full_q_num, int32_t *full_q_idx, void *stream) {
+  if (!gate || !code || !tile_class || !kv_num || !kv_idx || !full_kv_num || !full_kv_idx ||
+      !q_num || !q_idx || !full_q_num || !full_q_idx)
+    return fail(MGA_ERR_INVALID, "mga_mtp_block_mask: null pointer");
+  if (S <= 0 || P < 0 || gate_stride <= 0 || P + S > 0x7fffffffLL)
+    return fail(MGA_ERR_INVALID, "mga_mtp_block_mask: bad sizes (S=%d P=%lld stride=%lld)", S,
+                (long long)P, (long long)gate_stride);
+  mga::launch_mtp_block_mask(gate, gate_stride, S, P, code, tile_class, kv_num, kv_idx, full_kv_num,
+                             full_kv_idx, q_num, q_idx, full_q_num, full_q_idx, (hipStream_t)stream);
+  return check_launch("mga_mtp_block_mask");
+}
+
+int mga_attn_fwd(const void *q, int64_t q_sh, int64_t q_ss, const void *k, int64_t k_sh,
+                 int64_t k_ss, const void *v, int64_t v_sh, int64_t v_ss, void *o, int64_t o_sh,
+                 int64_t o_ss, float *lse, const int32_t *code, const int32_t *kv_num,
+                 const int32_t *kv_idx, const int32_t *full_kv_num, const int32_t *full_kv_idx,
+                 int32_t S, int32_t L, int32_t P, int32_t Hq, int32_t Hkv, int32_t head_dim,
+                 int32_t dtype, float scale, void *stream) {
+  int rc;
+  if ((rc = check_attn_common(S, L, P, Hq, Hkv, head_dim, dtype))) return rc;
+  const int eb = elem_bytes(dtype);
+  if ((rc = check_operand("q", q, q_sh, q_ss, eb))) return rc;
+  if ((rc = check_operand("k", k, k_sh, k_ss, eb))) return rc;
+  if ((rc = check_operand("v", v, v_sh, v_ss, eb))) return rc;
+  if ((rc = check_operand("o", o, o_sh, o_ss, eb))) return rc;
+  if (!lse || !code || !kv_num || !kv_idx || !full_kv_num || !full_kv_idx)
+    return fail(MGA_ERR_INVALID, "mga_attn_fwd: null lse/code/block-mask pointer");
+  mga::AttnArgs a = {};
+  a.q = q; a.q_sh = q_sh; a.q_ss = q_ss;
+  a.k = k; a.k_sh = k_sh; a.k_ss = k_ss;
+  a.v = v; a.v_sh = v_sh; a.v_ss = v_ss;
+  a.o = o; a.o_sh = o_sh; a.o_ss = o_ss;
+  a.lse = lse; a.code = code;
+  a.kv_num = kv_num; a.kv_idx = kv_idx; a.fkv_num = full_kv_num; a.fkv_idx = full_kv_idx;
+  a.S = S; a.L = L; a.P = P; a.Hq = Hq; a.Hkv = Hkv;
+  a.nQ = (S + MGA_BLOCK - 1) / MGA_BLOCK;
+  a.nKV = (L + MGA_BLOCK - 1) / MGA_BLOCK;
+  a.scale = scale;
+  a.scale_log2 = scale * mga::kLog2e;
+  mga::launch_attn_fwd(a, head_dim, dtype == MGA_DTYPE_F32, (hipStream_t)stream);
+  return check_launch("mga_attn_fwd");
+}
+
+int mga_attn_bwd(const void *q, int64_t q_sh, int64_t q_ss, const void *k, int64_t k_sh,
+                 int64_t k_ss, const void *v, int64_t v_sh, int64_t v_ss, const void *o,
+                 int64_t o_sh, int64_t o_ss, const void *dout, int64_t do_sh, int64_t do_ss,
+                 const float *lse, float *delta, void *dq, int64_t dq_sh, int64_t dq_ss, void *dk,
+                 int64_t dk_sh, int64_t dk_ss, void *dv, int64_t dv_sh, int64_t dv_ss,
+                 int32_t grad_start, const int32_t *code, const int32_t *kv_num,
+                 const int32_t *kv_idx, const int32_t *full_kv_num, const int32_t *full_kv_idx,
+                 const int32_t *q_num, const int32_t *q_idx, const int32_t *full_q_num,
+                 const int32_t *full_q_idx, int32_t S, int32_t L, int32_t P, int32_t Hq,
+                 int32_t Hkv, int32_t head_dim, int32_t dtype, float scale, void *stream) {
+  int rc;
+  if ((rc = check_attn_common(S, L, P, Hq, Hkv, head_dim, dtype))) return rc;
+  const int eb = elem_bytes(dtype);
+  if ((rc = check_operand("q", q, q_sh, q_ss, eb))) return rc;
+  if ((rc = check_operand("k", k, k_sh, k_ss, eb))) return rc;
+  if ((rc = check_operand("v", v, v_sh, v_ss, eb))) return rc;
+  if ((rc = check_operand("o", o, o_sh, o_ss, eb))) return rc;
+  if ((rc = check_operand("dout", dout, do_sh, do_ss, eb))) return rc;
+  if ((rc = check_operand("dq", dq, dq_sh, dq_ss, eb))) return rc;
+  if (grad_start < 0 || grad_start > L)
+    return fail(MGA_ERR_INVALID, "mga_attn_bwd: grad_start %d outside [0, L=%d]", grad_start, L);
+  if (grad_start < L) {
+    if ((rc = check_operand("dk", dk, dk_sh, dk_ss, eb))) return rc;
+    if ((rc = check_operand("dv", dv, dv_sh, dv_ss, eb))) return rc;
+  }
+  if (!lse || !delta || !code || !kv_num || !kv_idx || !full_kv_num || !full_kv_idx || !q_num ||
+      !q_idx || !full_q_num || !full_q_idx)
+    return fail(MGA_ERR_INVALID, "mga_attn_bwd: null lse/delta/code/block-mask pointer");
+  mga::AttnArgs a = {};
+  a.q = q; a.q_sh = q_sh; a.q_ss = q_ss;
+  a.k = k; a.k_sh = k_sh; a.k_ss = k_ss;
+  a.v = v; a.v_sh = v_sh; a.v_ss = v_ss;
+  a.o = o; a.o_sh = o_sh; a.o_ss = o_ss;
+  a.dout = dout; a.do_sh = do_sh; a.do_ss = do_ss;
+  a.lse = const_cast<float *>(lse); a.delta = delta;
+  a.dq = dq; a.dq_sh = dq_sh; a.dq_ss = dq_ss;
+  a.dk = dk; a.dk_sh = dk_sh; a.dk_ss = dk_ss;
+  a.dv = dv; a.dv_sh = dv_sh; a.dv_ss = dv_ss;
+  a.grad_start = grad_start; a.code = code;
+  a.kv_num = kv_num; a.kv_idx = kv_idx; a.fkv_num = full_kv_num; a.fkv_idx = full_kv_idx;
+  a.q_num = q_num; a.q_idx = q_idx; a.fq_num = full_q_num; a.fq_idx = full_q_idx;
+  a.S = S; a.L = L; a.P = P; a.Hq = Hq; a.Hkv = Hkv;
+  a.nQ = (S + MGA_BLOCK - 1) / MGA_BLOCK;
+  a.nKV = (L + MGA_BLOCK - 1) / MGA_BLOCK;
+  a.scale = scale;
+  a.scale_log2 = scale * mga::kLog2e;
+  mga::launch_attn_bwd(a, head_dim, dtype == MGA_DTYPE_F32, (hipStream_t)stream);
+  return check_launch("mga_attn_bwd");
+}
+
+}  // extern "C"

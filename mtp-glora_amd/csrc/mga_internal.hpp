@@ -1,0 +1,46 @@
+// Host-side launchers shared between the kernel files and the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mga {
+
+struct AttnArgs {
+  const void *q; int64_t q_sh, q_ss;
+  const void *k; int64_t k_sh, k_ss;
+  const void *v; int64_t v_sh, v_ss;
+  const void *o; int64_t o_sh, o_ss;      // fwd: output; bwd: saved output
+  const void *dout; int64_t do_sh, do_ss;
+  float *lse;                               // [Hq, S] natural log
+  float *delta;                             // [Hq, S] workspace (bwd)
+  void *dq; int64_t dq_sh, dq_ss;
+  void *dk; int64_t dk_sh, dk_ss;
+  void *dv; int64_t dv_sh, dv_ss;
+  int32_t grad_start;
+  const int32_t *code;
+  const int32_t *kv_num, *kv_idx, *fkv_num, *fkv_idx;
+  const int32_t *q_num, *q_idx, *fq_num, *fq_idx;
+  int32_t S, L, P, Hq, Hkv, nQ, nKV;
+  float scale, scale_log2;
+};
+
+void launch_kv_copy_rows(const void *src_k, const void *src_v, int64_t src_sh_b, int64_t src_ss_b,
+                         const int32_t *idx, int32_t n_rows, void *dst_k, void *dst_v,
+                         int64_t dst_sh_b, int64_t dst_ss_b, int64_t dst_off, int32_t n_heads,
+                         int32_t row_bytes, hipStream_t stream);
+
+void launch_regular_index(const int64_t *mask, int64_t stride, int32_t n, int32_t *idx,
+                          int32_t *count, hipStream_t stream);
+
+void launch_mtp_block_mask(const int64_t *gate, int64_t gate_stride, int32_t S, int64_t P,
+                           int32_t *code, int8_t *cls, int32_t *kv_num, int32_t *kv_idx,
+                           int32_t *full_kv_num, int32_t *full_kv_idx, int32_t *q_num,
+                           int32_t *q_idx, int32_t *full_q_num, int32_t *full_q_idx,
+                           hipStream_t stream);
+
+// head_dim in {64, 128}; is_f32 selects fp32 operands (else bf16).
+void launch_attn_fwd(const AttnArgs &a, int head_dim, bool is_f32, hipStream_t stream);
+void launch_attn_bwd(const AttnArgs &a, int head_dim, bool is_f32, hipStream_t stream);
+
+}  // namespace mga

@@ -1,0 +1,118 @@
+"""``StreamingKVCacheManager`` with the reference's three public methods
+(mtp_glora/data_utils/collator.py:178-287), driven by the trainer's chunk loop
+(mtp_glora/trainer/trainer.py:95-136):
+
+* ``reset_cache()``                              (collator.py:188-190)
+* ``prepare_data_with_kv_cache(chunk)``          (collator.py:193-217)
+* ``extract_regular_kv_cache_for_next_chunk(chunk, past_key_values)`` (collator.py:220-287)
+
+The BlockMask is built on the GPU from the unclamped gate (pad = -1), and only
+then is the gate clamped and unsqueezed for the LoRA gating (collator.py:208-215).
+The carry-over keeps the chunk's regular-token K/V in the preallocated cache
+in place instead of re-concatenating the prefix.
+"""
+from __future__ import annotations
+
+import warnings
+
+import torch
+
+from . import ops
+from .block_mask import build_mtp_block_mask
+from .cache import DEFAULT_CAPACITY, StreamingKVCache
+
+
+class StreamingKVCacheManager:
+    """KV cache manager for streaming/sequential chunk processing."""
+
+    def __init__(self, capacity: int = DEFAULT_CAPACITY, sanity_check: bool = True):
+        self.past_seen_tokens = 0
+        self.capacity = int(capacity)
+        self.sanity_check = sanity_check
+        self.cache: StreamingKVCache | None = None
+
+    def reset_cache(self) -> None:
+        """Reset KV cache for a new sequence (buffers stay allocated)."""
+        self.past_seen_tokens = 0
+        if self.cache is not None:
+            self.cache.reset()
+
+    def new_cache(self, num_layers: int) -> StreamingKVCache:
+        """The manager's cache, reset, for a model with ``num_layers`` layers;
+        pass it as ``past_key_values`` of the first chunk to skip the model's
+        own DynamicCache."""
+        if self.cache is None or self.cache.num_layers != num_layers:
+            self.cache = StreamingKVCache(capacity=self.capacity, num_layers=num_layers)
+        self.cache.reset()
+        self.past_seen_tokens = 0
+        return self.cache
+
+    def prepare_data_with_kv_cache(self, chunk_data: dict) -> dict:
+        """Attach the chunk's MTP BlockMask (against ``past_seen_tokens`` cached
+        tokens) as ``attention_mask``, then clamp the gate to >= 0 and unsqueeze
+        it for the LoRA gating."""
+        gate = chunk_data["gate_mask"]
+        if gate.shape[0] > 1:
+            warnings.warn("`prepare_data_with_kv_cache` expects batch size to be 1, "
+                          f"but got batch size: {gate.shape[0]}")
+        bm = build_mtp_block_mask(gate[:1], self.past_seen_tokens)
+        chunk_data["attention_mask"] = bm.to(chunk_data["input_ids"].device)
+        chunk_data["gate_mask"] = torch.clamp(chunk_data["gate_mask"], min=0)[:, :, None]
+        return chunk_data
+
+    def extract_regular_kv_cache_for_next_chunk(self, chunk_data: dict, past_key_values=None):
+        """Keep only the chunk's regular-token K/V (detached) behind the cached
+        prefix and advance ``past_seen_tokens``. Returns the cache to pass as
+        ``past_key_values`` of the next chunk."""
+        bsz = chunk_data["input_ids"].shape[0]
+        if bsz > 1:
+            warnings.warn("`extract_regular_kv_cache_for_next_chunk` expects batch size to be 1, "
+                          f"but got batch size: {bsz}")
+        if past_key_values is None:
+            return None
+        reg = chunk_data["regular_token_mask"][0]
+        idx, cnt = ops.regular_index(reg)
+        R = int(cnt.item())   # one host sync, as the reference's nonzero()
+
+        if self.sanity_check and "position_ids" in chunk_data:
+            pos = chunk_data["position_ids"][0]
+            got = pos[idx[:R].long()]
+            expected = torch.arange(self.past_seen_tokens, self.past_seen_tokens + R, device=pos.device)
+            if not torch.equal(got, expected.to(got.dtype)):
+                print("extract_regular_kv_cache_for_next_chunk: Sanity check failed. Position IDs mismatch. "
+                      f"Expected: {expected}, Actual: {got}")
+                print(f"self.past_seen_tokens: {self.past_seen_tokens}, num_new_regular_tokens: {R}")
+
+        if isinstance(past_key_values, StreamingKVCache):
+            cache = past_key_values
+            if cache.prefix_len != self.past_seen_tokens:
+                raise RuntimeError(f"cache holds {cache.prefix_len} prefix tokens but the manager "
+                                   f"has seen {self.past_seen_tokens}")
+            cache.commit_regular(idx, R)
+        else:
+            cache = self._take_over(past_key_values, chunk_data["input_ids"].shape[1], idx, R)
+        self.cache = cache
+        self.past_seen_tokens += R
+        return cache
+
+    def _take_over(self, past_key_values, chunk_len: int, idx: torch.Tensor, R: int) -> StreamingKVCache:
+        """Move a transformers DynamicCache / legacy tuple (the model builds one
+        when the first chunk gets ``past_key_values=None``) into the streaming
+        cache: its prefix rows, then the chunk's regular rows."""
+        layers = [(kv[0], kv[1]) for kv in past_key_values]
+        n = len(layers)
+        if self.cache is None or self.cache.num_layers != n:
+            self.cache = StreamingKVCache(capacity=self.capacity, num_layers=n)
+        cache = self.cache
+        cache.reset()
+        P = self.past_seen_tokens
+        for li, (k, v) in enumerate(layers):
+            if k.shape[2] != P + chunk_len:
+                raise RuntimeError(f"layer {li} holds {k.shape[2]} tokens, expected {P} + {chunk_len}")
+        if P > 0:
+            cache.append_prefix([k[:, :, :P] for k, _ in layers], [v[:, :, :P] for _, v in layers])
+        for li, (k, v) in enumerate(layers):
+            cache._ensure(li, k)
+            cache._staged[li] = (k[:, :, P:], v[:, :, P:])
+        cache.commit_regular(idx, R)
+        return cache

@@ -1,0 +1,82 @@
+"""Shared builders for the GPU parity tests (seeded synthetic chunks and the
+oracle comparisons with the stated bf16 tolerance)."""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from oracle import mtp_oracle as mo
+
+# Tolerance for attention outputs and gradients against the reference:
+# max-abs error <= 2e-2 and mean-abs error <= 2e-3.
+MAX_ABS = 2e-2
+MEAN_ABS = 2e-3
+
+
+def chunk_layout(n_reg, n_anchor, draft, P, seed=0, pad=0, tail=False, every=None):
+    if every is not None:
+        anchors = np.arange(0, n_reg, every)[:n_anchor]
+    else:
+        anchors = mo.sample_anchors(n_reg, n_anchor, seed)
+    seq = mo.synth_sequence(n_reg, anchors, draft, pos0=P, tail_unlabelled=tail)
+    return mo.pad_to(seq, len(seq.gate) + pad)
+
+
+def qkv(S, P, Hq, Hkv, D, dtype, dev, seed=0, std=0.5):
+    """q/k/v in the projection layout [1, S, H, D] viewed as [1, H, S, D];
+    prefix K/V [1, Hkv, P, D]; dO ~ N(0, 1) in [1, S, Hq, D]."""
+    gens = [torch.Generator(device=dev).manual_seed(seed * 16 + i) for i in range(6)]
+    r = lambda shape, g, s: (torch.randn(*shape, generator=g, device=dev) * s).to(dtype)
+    q = r((1, S, Hq, D), gens[0], std).transpose(1, 2)
+    k = r((1, S, Hkv, D), gens[1], std).transpose(1, 2)
+    v = r((1, S, Hkv, D), gens[2], std).transpose(1, 2)
+    kp = r((1, Hkv, P, D), gens[3], std)
+    vp = r((1, Hkv, P, D), gens[4], std)
+    do = r((1, S, Hq, D), gens[5], 1.0)
+    return q, k, v, kp, vp, do
+
+
+def f64(t):
+    return t.detach().double().cpu().numpy()
+
+
+def check(name, got, ref, max_abs=MAX_ABS, mean_abs=MEAN_ABS):
+    err = np.abs(np.asarray(got, np.float64) - np.asarray(ref, np.float64))
+    mx, mn = float(err.max()) if err.size else 0.0, float(err.mean()) if err.size else 0.0
+    print(f"  {name}: max-abs {mx:.3e} mean-abs {mn:.3e}", flush=True)
+    assert np.isfinite(got).all(), f"{name} has non-finite values"
+    assert mx <= max_abs and mn <= mean_abs, f"{name}: max-abs {mx:.3e} mean-abs {mn:.3e}"
+
+
+def torch_dense_reference(q, kfull, vfull, allowed, scale, do=None, grad_start=0):
+    """fp32 dense masked attention on the GPU with autograd, one query head at
+    a time (for shapes the float64 numpy oracle is too slow for). Inputs are
+    the kernel's own bf16 values upcast to fp32; the prefix gets no gradient."""
+    Hq, S, D = q.shape[1], q.shape[2], q.shape[3]
+    Hkv = kfull.shape[1]
+    G = Hq // Hkv
+    m = torch.as_tensor(allowed, device=q.device)
+    rowok = m.any(dim=1)
+    o = torch.empty(Hq, S, D, device=q.device, dtype=torch.float32)
+    lse = torch.empty(Hq, S, device=q.device, dtype=torch.float32)
+    dq = torch.empty_like(o) if do is not None else None
+    L = kfull.shape[2]
+    dk = torch.zeros(Hkv, L - grad_start, D, device=q.device) if do is not None else None
+    dv = torch.zeros_like(dk) if do is not None else None
+    for h in range(Hq):
+        g = h // G
+        qh = q[0, h].float().detach().requires_grad_(do is not None)
+        kh = kfull[0, g].float().detach().requires_grad_(do is not None)
+        vh = vfull[0, g].float().detach().requires_grad_(do is not None)
+        s = (qh @ kh.T) * scale
+        s = s.masked_fill(~m, float("-inf"))
+        lse[h] = torch.where(rowok, torch.logsumexp(s, dim=1), torch.full_like(lse[h], float("-inf"))).detach()
+        p = torch.where(rowok[:, None], torch.softmax(s.masked_fill(~rowok[:, None], 0.0), dim=1), 0.0)
+        oh = p @ vh
+        o[h] = oh.detach()
+        if do is not None:
+            oh.backward(do[0, :, h].float())
+            dq[h] = qh.grad
+            dk[g] += kh.grad[grad_start:]
+            dv[g] += vh.grad[grad_start:]
+    return o, lse, dq, dk, dv

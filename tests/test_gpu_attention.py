@@ -1,0 +1,140 @@
+"""HIP MTP attention forward/backward against the float64 CPU oracle (small
+and medium shapes) and an fp32 torch dense reference on the GPU (full config
+sizes). Tolerance: max-abs <= 2e-2, mean-abs <= 2e-3 on outputs and on every
+gradient; LSE within the same bounds; cache contents bit-exact."""
+import numpy as np
+import pytest
+import torch
+
+from gpu_helpers import MAX_ABS, MEAN_ABS, check, chunk_layout, f64, qkv, torch_dense_reference
+from oracle import mtp_oracle as mo
+
+pytestmark = pytest.mark.gpu
+
+
+def run_case(mga, dev, n_reg, n_anchor, draft, P, Hq, Hkv, D, dtype=torch.bfloat16, seed=0,
+             pad=0, tail=False, every=None, use_cache=True):
+    print(f"case n_reg={n_reg} anchors={n_anchor} draft={draft} P={P} Hq={Hq} Hkv={Hkv} D={D} "
+          f"{dtype} pad={pad} tail={tail} cache={use_cache}", flush=True)
+    seq = chunk_layout(n_reg, n_anchor, draft, P, seed=seed, pad=pad, tail=tail, every=every)
+    S = len(seq.gate)
+    q, k, v, kp, vp, do = qkv(S, P, Hq, Hkv, D, dtype, dev, seed=seed)
+    q.requires_grad_()
+    k.requires_grad_()
+    v.requires_grad_()
+    bm = mga.build_mtp_block_mask(torch.tensor(seq.gate, device=dev)[None], P)
+    if use_cache:
+        cache = mga.StreamingKVCache(capacity=P + S + 64, num_layers=1)
+        if P:
+            cache.append_prefix([kp], [vp])
+        kf, vf = cache.update(k, v, 0)
+    else:
+        kf = torch.cat([kp, k], dim=2)
+        vf = torch.cat([vp, v], dim=2)
+    o, lse = mga.mtp_attention(q, kf, vf, bm, D ** -0.5)
+    o.backward(do)
+    torch.cuda.synchronize()
+    return seq, q, k, v, kp, vp, do, o, lse
+
+
+def compare_oracle(seq, P, q, k, v, kp, vp, do, o, lse, D, grad_start):
+    allowed = mo.mtp_mask_dense(seq.gate, P)
+    qn = f64(q)[0]
+    kn = np.concatenate([f64(kp)[0], f64(k)[0]], axis=1)
+    vn = np.concatenate([f64(vp)[0], f64(v)[0]], axis=1)
+    on, lsen = mo.attention_fwd(qn, kn, vn, allowed, D ** -0.5)
+    check("o", f64(o)[0].transpose(1, 0, 2), on)
+    got_lse = f64(lse)[0]
+    assert np.array_equal(np.isneginf(got_lse), np.isneginf(lsen))
+    fin = np.isfinite(lsen)
+    check("lse", got_lse[fin], lsen[fin])
+    dqn, dkn, dvn = mo.attention_bwd(qn, kn, vn, on, lsen, f64(do)[0].transpose(1, 0, 2),
+                                     allowed, D ** -0.5, grad_start=grad_start)
+    check("dq", f64(q.grad)[0], dqn)
+    check("dk", f64(k.grad)[0], dkn[:, -k.shape[2]:])
+    check("dv", f64(v.grad)[0], dvn[:, -v.shape[2]:])
+
+
+SMALL = [
+    dict(n_reg=256, n_anchor=16, draft=4, P=0, Hq=4, Hkv=2, D=128),
+    dict(n_reg=256, n_anchor=16, draft=4, P=256, Hq=4, Hkv=2, D=128),
+    dict(n_reg=300, n_anchor=25, draft=4, P=200, Hq=8, Hkv=2, D=128, pad=37),   # ragged S and P
+    dict(n_reg=200, n_anchor=50, draft=8, P=384, Hq=4, Hkv=1, D=128),           # mask heavy, G=4
+    dict(n_reg=256, n_anchor=16, draft=4, P=128, Hq=4, Hkv=2, D=64),            # config-1 head_dim
+    dict(n_reg=180, n_anchor=20, draft=4, P=96, Hq=2, Hkv=2, D=64, tail=True, pad=20),  # MHA
+    dict(n_reg=60, n_anchor=5, draft=2, P=0, Hq=4, Hkv=2, D=128, pad=3),        # S < 128
+]
+
+
+@pytest.mark.parametrize("c", SMALL)
+def test_attention_small_bf16(mga, dev, c):
+    out = run_case(mga, dev, **c)
+    seq, q, k, v, kp, vp, do, o, lse = out
+    compare_oracle(seq, c["P"], q, k, v, kp, vp, do, o, lse, c["D"], grad_start=c["P"])
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_attention_fp32_operands(mga, dev, D):
+    c = dict(n_reg=256, n_anchor=16, draft=4, P=128, Hq=4, Hkv=2, D=D)
+    seq, q, k, v, kp, vp, do, o, lse = run_case(mga, dev, dtype=torch.float32, **c)
+    assert o.dtype == torch.float32 and q.grad.dtype == torch.float32
+    compare_oracle(seq, c["P"], q, k, v, kp, vp, do, o, lse, D, grad_start=c["P"])
+
+
+def test_plain_key_tensor_gets_full_gradient(mga, dev):
+    """Keys passed as one plain tensor (e.g. from a DynamicCache): every key
+    row, prefix included, receives its gradient."""
+    c = dict(n_reg=200, n_anchor=20, draft=4, P=128, Hq=4, Hkv=2, D=128)
+    seq = chunk_layout(200, 20, 4, 128, seed=4)
+    S = len(seq.gate)
+    q, k, v, kp, vp, do = qkv(S, 128, 4, 2, 128, torch.bfloat16, dev, seed=4)
+    kf = torch.cat([kp, k], dim=2).requires_grad_()
+    vf = torch.cat([vp, v], dim=2).requires_grad_()
+    q.requires_grad_()
+    bm = mga.build_mtp_block_mask(torch.tensor(seq.gate, device=dev)[None], 128)
+    o, lse = mga.mtp_attention(q, kf, vf, bm, 128 ** -0.5)
+    o.backward(do)
+    allowed = mo.mtp_mask_dense(seq.gate, 128)
+    on, lsen = mo.attention_fwd(f64(q)[0], f64(kf)[0], f64(vf)[0], allowed, 128 ** -0.5)
+    dqn, dkn, dvn = mo.attention_bwd(f64(q)[0], f64(kf)[0], f64(vf)[0], on, lsen,
+                                     f64(do)[0].transpose(1, 0, 2), allowed, 128 ** -0.5)
+    check("o", f64(o)[0].transpose(1, 0, 2), on)
+    check("dq", f64(q.grad)[0], dqn)
+    check("dk", f64(kf.grad)[0], dkn)
+    check("dv", f64(vf.grad)[0], dvn)
+
+
+def test_transformers_wrapper_contract(mga, dev):
+    """Output [B, S, Hq, D] contiguous and LSE cast to the value dtype, as
+    flex_attention_forward returns ([tf]integrations/flex_attention.py:346, 367)."""
+    seq = chunk_layout(128, 8, 4, 0, seed=5)
+    S = len(seq.gate)
+    q, k, v, *_ = qkv(S, 0, 4, 2, 128, torch.bfloat16, dev)
+    bm = mga.build_mtp_block_mask(torch.tensor(seq.gate, device=dev)[None], 0)
+    o, lse = mga.mtp_attention_forward(torch.nn.Module(), q, k, v, bm, scaling=0.1, dropout=0.0,
+                                       sliding_window=None)
+    assert o.shape == (1, S, 4, 128) and o.is_contiguous() and lse.dtype == torch.bfloat16
+
+
+@pytest.mark.parametrize("cfg", [
+    dict(name="config2", n_reg=4096, n_anchor=256, draft=4, P=8192),
+    dict(name="config5", n_reg=2048, n_anchor=512, draft=8, P=16384, every=4),
+])
+def test_attention_full_config(mga, dev, cfg):
+    """Full Qwen3-8B attention geometry (32 q / 8 kv heads, D = 128) against an
+    fp32 dense reference on the GPU fed the same bf16 values."""
+    Hq, Hkv, D = 32, 8, 128
+    seq, q, k, v, kp, vp, do, o, lse = run_case(
+        mga, dev, cfg["n_reg"], cfg["n_anchor"], cfg["draft"], cfg["P"], Hq, Hkv, D, seed=2,
+        every=cfg.get("every"))
+    P = cfg["P"]
+    allowed = mo.mtp_mask_dense(seq.gate, P)
+    kfull = torch.cat([kp, k.detach()], dim=2)
+    vfull = torch.cat([vp, v.detach()], dim=2)
+    ro, rlse, rdq, rdk, rdv = torch_dense_reference(q.detach(), kfull, vfull, allowed, D ** -0.5,
+                                                    do=do, grad_start=P)
+    check("o", f64(o)[0].transpose(1, 0, 2), ro.cpu().numpy())
+    check("lse", f64(lse)[0], rlse.cpu().numpy())
+    check("dq", f64(q.grad)[0], rdq.cpu().numpy())
+    check("dk", f64(k.grad)[0], rdk.cpu().numpy())
+    check("dv", f64(v.grad)[0], rdv.cpu().numpy())
