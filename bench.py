@@ -1,0 +1,339 @@
+#!/usr/bin/env python3
+"""Benchmark of the chunked-training hot path on one MI355X.
+
+Metric: masked-attention fwd+bwd TFLOP/s and KV-append GB/s
+per chunk at Qwen3-8B attention geometry. Workload: config 2 (one layer,
+32 query / 8 KV heads, head_dim 128, bf16; a 8192-token cached prefix; a chunk
+of 4096 regular tokens + 256 anchors x 4 mask tokens = 5120 query rows).
+
+One step is one layer-chunk through the drop-in boundary, exactly as the
+trainer's chunk loop drives it (mtp_glora/trainer/trainer.py:95-136):
+  prepare_data_with_kv_cache (MTP block mask on the GPU) -> cache.update (stage
+  the chunk's K/V after the prefix) -> attention forward -> backward (dQ, and
+  dK/dV of the chunk's keys) -> extract_regular_kv_cache_for_next_chunk
+  (regular-token index + gather-append of the 4096 regular rows),
+then the cache is cropped back to the same prefix so every step is identical.
+Inputs are resident in HBM before the timed region.
+
+``value`` = credited attention FLOPs per step / measured step time (the whole
+step: mask build, appends and attention). The credited FLOPs count only the
+non-empty 128x128 tiles of the reference BlockMask and no dK/dV for the
+detached prefix: Hq*D*[4(A_pre+A_cur) + 6 A_pre + 10 A_cur]. Per-kernel
+durations (HIP events on the launch stream) give the roofline fractions.
+
+``cpu_baseline``: the reference's CPU path (torch flex_attention eager -- the
+dense math path -- fwd + autograd bwd on the restated MTP mask_mod) on one
+KV-head group (4 query heads, full S and P+S), median of timed runs.
+"""
+from __future__ import annotations
+
+import argparse
+import importlib
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+METRIC = "masked-attn fwd+bwd TFLOP/s + KV append GB/s per chunk, Qwen3-8B shape, 1 GPU"
+PEAK_MFMA_BF16_TFLOPS = 2516.6   # MI355X dense bf16 MFMA
+PEAK_HBM_GBPS = 8000.0           # MI355X HBM3E
+
+CONFIGS = {
+    2: dict(workload="config2: Qwen3-8B single layer, 4096 regular + 256x4 mask rows vs 8192-token prefix",
+            Hq=32, Hkv=8, D=128, P=8192, n_reg=4096, n_anchor=256, draft=4, every=None),
+    5: dict(workload="config5: Qwen3-4B dense MTP, 2048 regular + 512x8 mask rows vs 16384-token prefix",
+            Hq=32, Hkv=8, D=128, P=16384, n_reg=2048, n_anchor=512, draft=8, every=4),
+}
+SEED = 1234
+
+
+def tile_areas(bm, S: int, L: int, P: int, block: int = 128):
+    """(A_pre, A_cur): clipped areas of the non-empty tiles of the block mask,
+    split at the prefix boundary P."""
+    kv_num = bm.kv_num_blocks[0, 0].tolist()
+    kv_idx = bm.kv_indices[0, 0].tolist()
+    fkv_num = bm.full_kv_num_blocks[0, 0].tolist()
+    fkv_idx = bm.full_kv_indices[0, 0].tolist()
+    a_pre = a_cur = 0
+    for qt in range(len(kv_num)):
+        rows = min(block, S - qt * block)
+        for kt in kv_idx[qt][:kv_num[qt]] + fkv_idx[qt][:fkv_num[qt]]:
+            k0, k1 = kt * block, min(L, kt * block + block)
+            npre = max(0, min(k1, P) - k0)
+            a_pre += rows * npre
+            a_cur += rows * (k1 - k0 - npre)
+    return a_pre, a_cur
+
+
+class EventTimer:
+    """Average duration of a callable's GPU work over ``n`` back-to-back runs,
+    from HIP events recorded on the stream the kernels are launched on."""
+
+    def __init__(self, torch):
+        self.torch = torch
+
+    def __call__(self, fn, n: int) -> float:
+        torch = self.torch
+        st = torch.cuda.current_stream()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        fn()
+        torch.cuda.synchronize()
+        e0.record(st)
+        for _ in range(n):
+            fn()
+        e1.record(st)
+        e1.synchronize()
+        return e0.elapsed_time(e1) / n
+
+
+def graph_time(torch, fn, n: int, reps: int = 5) -> float:
+    """Average duration of ``fn`` captured ``n`` times into one HIP graph
+    (removes host launch gaps from microsecond kernels)."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(n):
+            fn()
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    st = torch.cuda.current_stream()
+    e0.record(st)
+    for _ in range(reps):
+        g.replay()
+    e1.record(st)
+    e1.synchronize()
+    return e0.elapsed_time(e1) / (n * reps)
+
+
+def cpu_baseline(cfg: dict, gate_cpu, reps: int, heads: int) -> dict:
+    """The reference's CPU attention path on one KV-head group."""
+    import torch
+    from oracle import flex_ref as fr
+    threads = min(os.cpu_count() or 1, 16)
+    torch.set_num_threads(threads)
+    P, D = cfg["P"], cfg["D"]
+    S = gate_cpu.shape[1]
+    L = P + S
+    t0 = time.perf_counter()
+    bm = fr.reference_block_mask(gate_cpu, P)
+    mask_s = time.perf_counter() - t0
+    g = torch.Generator().manual_seed(SEED)
+    q = (torch.randn(1, heads, S, D, generator=g) * 0.5).bfloat16()
+    k = (torch.randn(1, 1, L, D, generator=g) * 0.5).bfloat16()
+    v = (torch.randn(1, 1, L, D, generator=g) * 0.5).bfloat16()
+    do = torch.randn(1, heads, S, D, generator=g).bfloat16()
+    import warnings
+    with warnings.catch_warnings():
+        warnings.simplefilter("ignore")
+        fr.reference_attention(q, k, v, bm, D ** -0.5, do=do)          # warm-up
+        times = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fr.reference_attention(q, k, v, bm, D ** -0.5, do=do)
+            times.append(time.perf_counter() - t0)
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return dict(seconds=statistics.median(times), times=times, mask_build_s=mask_s,
+                threads=torch.get_num_threads(), cpu_count=os.cpu_count(), cpu_model=model)
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", type=int, default=2, choices=sorted(CONFIGS))
+    ap.add_argument("--cpu-reps", type=int, default=3, help="timed runs of the CPU baseline (0 = skip)")
+    ap.add_argument("--cpu-heads", type=int, default=4, help="query heads in the CPU sample (one KV group)")
+    ap.add_argument("--phase-iters", type=int, default=20)
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build's hot path (streaming KV cache + MTP "
+              "attention) runs per GPU with no collectives; multi-GPU runs are not part of it.",
+              file=sys.stderr)
+        return 2
+
+    import torch
+    mga = importlib.import_module("mtp-glora_amd")
+    from importlib import import_module
+    syn = import_module("mtp-glora_amd.synthetic")
+    lib_ops = mga.ops
+    libc = import_module("mtp-glora_amd._lib")
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 1
+    mga.load_library()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    cfg = CONFIGS[args.config]
+    Hq, Hkv, D, P = cfg["Hq"], cfg["Hkv"], cfg["D"], cfg["P"]
+    n_reg = cfg["n_reg"]
+    if cfg["every"]:
+        anchors = syn.every_kth_anchor(n_reg, cfg["every"], cfg["n_anchor"])
+    else:
+        anchors = syn.sample_anchors(n_reg, cfg["n_anchor"], SEED)
+    chunk0 = syn.mtp_chunk(n_reg, anchors, cfg["draft"], pos0=P, device=dev, seed=SEED)
+    S = chunk0["gate_mask"].shape[1]
+    L = P + S
+    R = int(chunk0["regular_token_mask"].sum())
+    scale = D ** -0.5
+
+    gens = [torch.Generator(device=dev).manual_seed(SEED + i) for i in range(6)]
+    rnd = lambda shape, g, s: (torch.randn(*shape, generator=g, device=dev) * s).bfloat16()
+    # projection layout [1, S, H, D] seen as [1, H, S, D], as the adapters pass them
+    q = rnd((1, S, Hq, D), gens[0], 0.5).transpose(1, 2).requires_grad_()
+    k = rnd((1, S, Hkv, D), gens[1], 0.5).transpose(1, 2).requires_grad_()
+    v = rnd((1, S, Hkv, D), gens[2], 0.5).transpose(1, 2).requires_grad_()
+    kp = rnd((1, Hkv, P, D), gens[3], 0.5)
+    vp = rnd((1, Hkv, P, D), gens[4], 0.5)
+    do = rnd((1, S, Hq, D), gens[5], 1.0)
+
+    mgr = mga.StreamingKVCacheManager(capacity=L + 256, sanity_check=False)
+    cache = mgr.new_cache(num_layers=1)
+    cache.append_prefix([kp], [vp])
+    mgr.past_seen_tokens = P
+    module = torch.nn.Module()
+
+    def step():
+        chunk = dict(chunk0)
+        chunk = mgr.prepare_data_with_kv_cache(chunk)
+        kf, vf = cache.update(k, v, 0)
+        o, _ = mga.mtp_attention_forward(module, q, kf, vf, chunk["attention_mask"], scaling=scale)
+        grads = torch.autograd.grad(o, (q, k, v), do)
+        mgr.extract_regular_kv_cache_for_next_chunk(chunk, cache)
+        cache.crop(P)
+        mgr.past_seen_tokens = P
+        return grads
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t_host = time.perf_counter()
+    e0.record()
+    for _ in range(args.steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    host_ms = (time.perf_counter() - t_host) * 1e3 / args.steps
+    ms_per_step = e0.elapsed_time(e1) / args.steps
+
+    # ---- credited work ------------------------------------------------------
+    bm = mga.build_mtp_block_mask(chunk0["gate_mask"], P)
+    a_pre, a_cur = tile_areas(bm, S, L, P)
+    fl_fwd = Hq * D * 4 * (a_pre + a_cur)
+    fl_dq = Hq * D * 6 * (a_pre + a_cur)
+    fl_dkdv = Hq * D * 4 * a_cur
+    fl_total = fl_fwd + fl_dq + fl_dkdv
+    append_bytes = 2 * R * Hkv * D * 2 * 2        # read + write, K and V, bf16
+    stage_bytes = 2 * S * Hkv * D * 2 * 2
+
+    # ---- per-phase kernel timing (HIP events on the launch stream) ----------
+    timer = EventTimer(torch)
+    n = args.phase_iters
+    kbuf, vbuf = cache.key_buffer(0), cache.value_buffer(0)
+    code, bmt = bm.mtp_code, bm.kernel_tensors()
+    kf = kbuf[None, :, :L]
+    vf = vbuf[None, :, :L]
+    lib_ops.kv_append(k.detach(), v.detach(), kbuf, vbuf, dst_offset=P)
+    qd = q.detach()
+    o, lse = lib_ops.attn_fwd(qd, kf, vf, code, bmt, P, scale)
+    bufs = lib_ops.bwd_buffers(qd, kf, P)
+    idx, cnt = lib_ops.regular_index(chunk0["regular_token_mask"])
+    torch.cuda.synchronize()
+
+    t_mask = timer(lambda: mga.build_mtp_block_mask(chunk0["gate_mask"], P), n)
+    t_fwd = timer(lambda: lib_ops.attn_fwd(qd, kf, vf, code, bmt, P, scale), n)
+    t_dq = timer(lambda: lib_ops.attn_bwd(qd, kf, vf, o, lse, do, code, bmt, P, scale, P,
+                                          passes=libc.BWD_DQ, buffers=bufs), n)
+    t_dkdv = timer(lambda: lib_ops.attn_bwd(qd, kf, vf, o, lse, do, code, bmt, P, scale, P,
+                                            passes=libc.BWD_DKDV, buffers=bufs), n)
+    app_dst = torch.empty(Hkv, R + 16, D, dtype=torch.bfloat16, device=dev)
+    app_dst_v = torch.empty_like(app_dst)
+    t_commit = graph_time(torch, lambda: lib_ops.kv_append(k.detach(), v.detach(), app_dst, app_dst_v,
+                                                           dst_offset=0, idx=idx, n_rows=R), 50)
+    t_stage = graph_time(torch, lambda: lib_ops.kv_append(k.detach(), v.detach(), kbuf, vbuf,
+                                                          dst_offset=P), 50)
+    torch.cuda.synchronize()
+
+    phases = {"mask_build": t_mask, "fwd": t_fwd, "bwd_dq_pass": t_dq, "bwd_dkdv_pass": t_dkdv,
+              "append_commit": t_commit, "append_stage": t_stage}
+    credited = {"fwd": fl_fwd, "bwd_dq_pass": fl_dq, "bwd_dkdv_pass": fl_dkdv}
+    dom = max(credited, key=lambda kname: phases[kname])
+    attn_ms = t_fwd + t_dq + t_dkdv
+    dom_tflops = credited[dom] / (phases[dom] * 1e-3) / 1e12
+    commit_gbps = append_bytes / (t_commit * 1e-3) / 1e9
+
+    out = {
+        "metric": METRIC,
+        "value": round(fl_total / (ms_per_step * 1e-3) / 1e12, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": cfg["workload"], "Hq": Hq, "Hkv": Hkv, "head_dim": D, "prefix": P,
+                   "chunk_rows": S, "regular_rows": R, "anchors": int(anchors.numel()),
+                   "draft_length": cfg["draft"], "seed": SEED},
+        "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(dom_tflops, 2),
+                     "peak": PEAK_MFMA_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(dom_tflops / PEAK_MFMA_BF16_TFLOPS, 4), "traffic": None},
+        "attention": {"credited_gflop": {"fwd": fl_fwd / 1e9, "bwd": (fl_dq + fl_dkdv) / 1e9,
+                                         "total": fl_total / 1e9},
+                      "tiles_area": {"prefix": a_pre, "chunk": a_cur},
+                      "fwd_bwd_ms": round(attn_ms, 4),
+                      "fwd_bwd_tflops": round(fl_total / (attn_ms * 1e-3) / 1e12, 2),
+                      "fwd_bwd_frac": round(fl_total / (attn_ms * 1e-3) / 1e12 / PEAK_MFMA_BF16_TFLOPS, 4),
+                      "fwd_tflops": round(fl_fwd / (t_fwd * 1e-3) / 1e12, 2),
+                      "bwd_tflops": round((fl_dq + fl_dkdv) / ((t_dq + t_dkdv) * 1e-3) / 1e12, 2)},
+        "append": {"bytes": append_bytes, "ms": round(t_commit, 5), "GBps": round(commit_gbps, 1),
+                   "frac": round(commit_gbps / PEAK_HBM_GBPS, 4), "peak": PEAK_HBM_GBPS,
+                   "stage_GBps": round(stage_bytes / (t_stage * 1e-3) / 1e9, 1)},
+        "phases_ms": {kname: round(t, 5) for kname, t in phases.items()},
+        "host_ms_per_step": round(host_ms, 4),
+    }
+
+    if args.cpu_reps > 0:
+        cb = cpu_baseline(cfg, chunk0["gate_mask"].cpu(), args.cpu_reps, args.cpu_heads)
+        frac = args.cpu_heads / Hq
+        cpu_tflops = fl_total * frac / cb["seconds"] / 1e12
+        out["cpu_baseline"] = {
+            "value": round(cpu_tflops, 4), "unit": "TFLOP/s", "cores": cb["threads"], "kind": "port",
+            "sample": (f"torch flex_attention eager (dense math path) fwd+bwd on CPU with the restated "
+                       f"MTP mask_mod: {args.cpu_heads} query heads of one KV head at the full "
+                       f"S={S}, P+S={L}; median of {args.cpu_reps} runs after a warm-up; credited "
+                       f"FLOPs scaled by {args.cpu_heads}/{Hq}"),
+            "seconds": round(cb["seconds"], 3), "mask_build_s": round(cb["mask_build_s"], 3),
+            "cpu_count": cb["cpu_count"], "cpu_model": cb["cpu_model"],
+        }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -39,6 +39,9 @@ extern "C" {
 #define MGA_DTYPE_BF16 0
 #define MGA_DTYPE_F32 1
 
+#define MGA_BWD_DQ 1        /* mga_attn_bwd: delta = rowsum(o * dout), then dQ */
+#define MGA_BWD_DKDV 2      /* mga_attn_bwd: dK / dV (reads the delta of the dQ pass) */
+
 #define MGA_BLOCK 128       /* BlockMask tile edge, [torch]nn/attention/flex_attention.py:395 */
 
 /* Library version (major * 10000 + minor * 100 + patch). */
@@ -117,6 +120,9 @@ int mga_attn_fwd(const void *q, int64_t q_sh, int64_t q_ss,
  *   the G query heads of each kv head. With grad_start = P the detached
  *   prefix (collator.py:279-280) gets no gradient and costs no dK/dV work.
  * delta: workspace of Hq * S floats (rowsum(o * dout)).
+ * passes: MGA_BWD_DQ | MGA_BWD_DKDV for the full backward. MGA_BWD_DQ alone
+ *   serves a caller whose K/V need no gradient; the passes may also be issued
+ *   as two calls in stream order (MGA_BWD_DQ first: it writes delta).
  * Replaces flex_attention's backward ([torch]_higher_order_ops/flex_attention.py:826-990)
  * followed by the cat-backward of DynamicLayer.update.
  * dq, dk, dv are fully written (no accumulation into existing contents).
@@ -136,7 +142,7 @@ int mga_attn_bwd(const void *q, int64_t q_sh, int64_t q_ss,
                  const int32_t *q_num, const int32_t *q_idx,
                  const int32_t *full_q_num, const int32_t *full_q_idx,
                  int32_t S, int32_t L, int32_t P, int32_t Hq, int32_t Hkv,
-                 int32_t head_dim, int32_t dtype, float scale, void *stream);
+                 int32_t head_dim, int32_t dtype, float scale, int32_t passes, void *stream);
 
 #ifdef __cplusplus
 }

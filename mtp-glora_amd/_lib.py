@@ -18,6 +18,8 @@ MGA_ERR_CAPACITY = 2
 MGA_ERR_HIP = 3
 DTYPE_BF16 = 0
 DTYPE_F32 = 1
+BWD_DQ = 1
+BWD_DKDV = 2
 
 # name -> argtypes; every function returns int (status) unless listed in _RESTYPES
 _P = ctypes.c_void_p
@@ -37,7 +39,7 @@ SIGNATURES = {
                      _P, _P,
                      _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64,
                      _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P,
-                     _I32, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _P],
+                     _I32, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _I32, _P],
 }
 _RESTYPES = {"mga_last_error": ctypes.c_char_p}
 

@@ -20,7 +20,7 @@ from __future__ import annotations
 
 import torch
 
-from . import ops
+from . import _lib, ops
 from .block_mask import MTPBlockMask
 
 
@@ -51,8 +51,10 @@ class _MTPAttention(torch.autograd.Function):
         L = k_full.shape[2]
         need_kv = ctx.needs_input_grad[1] or ctx.needs_input_grad[2]
         grad_start = ctx.grad_start if need_kv else L
+        passes = _lib.BWD_DQ | (_lib.BWD_DKDV if need_kv else 0)
         dq, dk, dv = ops.attn_bwd(q, k_full, v_full, o, lse, do, mask.mtp_code,
-                                  mask.kernel_tensors(), mask.prefix_len, ctx.scale, grad_start)
+                                  mask.kernel_tensors(), mask.prefix_len, ctx.scale, grad_start,
+                                  passes=passes)
         dq = dq if ctx.needs_input_grad[0] else None
         dk = dk if ctx.needs_input_grad[1] else None
         dv = dv if ctx.needs_input_grad[2] else None

@@ -186,6 +186,19 @@ class StreamingKVCache:
         self._len = [self.prefix_len] * self.num_layers
         self._staged = [None] * self.num_layers
 
+    def crop(self, max_length: int) -> None:
+        """Keep only the first ``max_length`` cached prefix tokens (negative:
+        drop that many from the end), as transformers' ``Cache.crop``; a
+        staged chunk is discarded. The buffers stay allocated."""
+        if max_length < 0:
+            max_length = self.prefix_len + max_length
+        if max_length < 0:
+            raise ValueError("crop would leave a negative length")
+        self.prefix_len = min(self.prefix_len, int(max_length))
+        n = self.num_layers or 0
+        self._len = [self.prefix_len] * n if self._k is not None else []
+        self._staged = [None] * n if self._k is not None else []
+
     def append_prefix(self, keys, values) -> None:
         """Append already-filtered prefix rows (``[1, Hkv, n, D]`` per layer) for
         every layer, e.g. when taking over a legacy cache."""

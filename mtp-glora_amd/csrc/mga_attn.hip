@@ -566,14 +566,16 @@ static void fwd_impl(const AttnArgs &a, hipStream_t st) {
 }
 
 template <int HD, typename T>
-static void bwd_impl(const AttnArgs &a, hipStream_t st) {
+static void bwd_impl(const AttnArgs &a, int passes, hipStream_t st) {
   constexpr int RPB = 256 / (HD / 8);
   const int rows = a.S * a.Hq;
-  hipLaunchKernelGGL((attn_bwd_delta_kernel<HD, T>), dim3((rows + RPB - 1) / RPB), dim3(256), 0, st, a);
-  hipLaunchKernelGGL((attn_bwd_dq_kernel<HD, T>), dim3(a.nQ * a.Hq), dim3(128), 0, st, a);
+  if (passes & kBwdDq) {
+    hipLaunchKernelGGL((attn_bwd_delta_kernel<HD, T>), dim3((rows + RPB - 1) / RPB), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((attn_bwd_dq_kernel<HD, T>), dim3(a.nQ * a.Hq), dim3(128), 0, st, a);
+  }
   const int kt0 = a.grad_start / kBlock;
   const int nkt = a.nKV - kt0;
-  if (nkt > 0 && a.grad_start < a.L)
+  if ((passes & kBwdDkDv) && nkt > 0 && a.grad_start < a.L)
     hipLaunchKernelGGL((attn_bwd_dkdv_kernel<HD, T>), dim3(nkt * a.Hkv), dim3(256), 0, st, a, kt0, nkt);
 }
 
@@ -585,11 +587,11 @@ void launch_attn_fwd(const AttnArgs &a, int head_dim, bool is_f32, hipStream_t s
   }
 }
 
-void launch_attn_bwd(const AttnArgs &a, int head_dim, bool is_f32, hipStream_t st) {
+void launch_attn_bwd(const AttnArgs &a, int head_dim, bool is_f32, int passes, hipStream_t st) {
   if (head_dim == 128) {
-    if (is_f32) bwd_impl<128, float>(a, st); else bwd_impl<128, bf16_t>(a, st);
+    if (is_f32) bwd_impl<128, float>(a, passes, st); else bwd_impl<128, bf16_t>(a, passes, st);
   } else {
-    if (is_f32) bwd_impl<64, float>(a, st); else bwd_impl<64, bf16_t>(a, st);
+    if (is_f32) bwd_impl<64, float>(a, passes, st); else bwd_impl<64, bf16_t>(a, passes, st);
   }
 }
 

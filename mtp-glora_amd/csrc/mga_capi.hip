@@ -7,6 +7,8 @@
 #include "mga_common.hpp"
 #include "mga_internal.hpp"
 
+static_assert(MGA_BWD_DQ == mga::kBwdDq && MGA_BWD_DKDV == mga::kBwdDkDv, "pass flags");
+
 namespace {
 
 thread_local char g_err[1024] = {0};
@@ -155,19 +157,22 @@ int mga_attn_bwd(const void *q, int64_t q_sh, int64_t q_ss, const void *k, int64
                  const int32_t *kv_idx, const int32_t *full_kv_num, const int32_t *full_kv_idx,
                  const int32_t *q_num, const int32_t *q_idx, const int32_t *full_q_num,
                  const int32_t *full_q_idx, int32_t S, int32_t L, int32_t P, int32_t Hq,
-                 int32_t Hkv, int32_t head_dim, int32_t dtype, float scale, void *stream) {
+                 int32_t Hkv, int32_t head_dim, int32_t dtype, float scale, int32_t passes,
+                 void *stream) {
   int rc;
   if ((rc = check_attn_common(S, L, P, Hq, Hkv, head_dim, dtype))) return rc;
+  if (passes <= 0 || (passes & ~(MGA_BWD_DQ | MGA_BWD_DKDV)))
+    return fail(MGA_ERR_INVALID, "mga_attn_bwd: passes must be a non-empty set of MGA_BWD_DQ | MGA_BWD_DKDV (got %d)", passes);
   const int eb = elem_bytes(dtype);
   if ((rc = check_operand("q", q, q_sh, q_ss, eb))) return rc;
   if ((rc = check_operand("k", k, k_sh, k_ss, eb))) return rc;
   if ((rc = check_operand("v", v, v_sh, v_ss, eb))) return rc;
   if ((rc = check_operand("o", o, o_sh, o_ss, eb))) return rc;
   if ((rc = check_operand("dout", dout, do_sh, do_ss, eb))) return rc;
-  if ((rc = check_operand("dq", dq, dq_sh, dq_ss, eb))) return rc;
+  if ((passes & MGA_BWD_DQ) && (rc = check_operand("dq", dq, dq_sh, dq_ss, eb))) return rc;
   if (grad_start < 0 || grad_start > L)
     return fail(MGA_ERR_INVALID, "mga_attn_bwd: grad_start %d outside [0, L=%d]", grad_start, L);
-  if (grad_start < L) {
+  if ((passes & MGA_BWD_DKDV) && grad_start < L) {
     if ((rc = check_operand("dk", dk, dk_sh, dk_ss, eb))) return rc;
     if ((rc = check_operand("dv", dv, dv_sh, dv_ss, eb))) return rc;
   }
@@ -192,7 +197,7 @@ int mga_attn_bwd(const void *q, int64_t q_sh, int64_t q_ss, const void *k, int64
   a.nKV = (L + MGA_BLOCK - 1) / MGA_BLOCK;
   a.scale = scale;
   a.scale_log2 = scale * mga::kLog2e;
-  mga::launch_attn_bwd(a, head_dim, dtype == MGA_DTYPE_F32, (hipStream_t)stream);
+  mga::launch_attn_bwd(a, head_dim, dtype == MGA_DTYPE_F32, passes, (hipStream_t)stream);
   return check_launch("mga_attn_bwd");
 }
 

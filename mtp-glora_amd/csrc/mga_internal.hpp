@@ -41,6 +41,9 @@ void launch_mtp_block_mask(const int64_t *gate, int64_t gate_stride, int32_t S, 
 
 // head_dim in {64, 128}; is_f32 selects fp32 operands (else bf16).
 void launch_attn_fwd(const AttnArgs &a, int head_dim, bool is_f32, hipStream_t stream);
-void launch_attn_bwd(const AttnArgs &a, int head_dim, bool is_f32, hipStream_t stream);
+// passes: kBwdDq (delta + dQ) and/or kBwdDkDv (dK/dV; reads the delta the dQ pass wrote).
+constexpr int kBwdDq = 1;
+constexpr int kBwdDkDv = 2;
+void launch_attn_bwd(const AttnArgs &a, int head_dim, bool is_f32, int passes, hipStream_t stream);
 
 }  // namespace mga

@@ -175,11 +175,28 @@ def attn_fwd(q, k, v, code, bm: dict, P: int, scale: float):
     return o, lse
 
 
+def bwd_buffers(q, k, grad_start: int) -> dict:
+    """Output and workspace buffers of ``attn_bwd``: dq [1, S, Hq, D], dk/dv
+    [1, L - grad_start, Hkv, D] (None when grad_start == L), delta [Hq * S] fp32."""
+    _, Hq, S, D = q.shape
+    _, Hkv, L, _ = k.shape
+    dev, dt = q.device, q.dtype
+    Lg = L - grad_start
+    return dict(dq=torch.empty(1, S, Hq, D, dtype=dt, device=dev),
+                dk=torch.empty(1, Lg, Hkv, D, dtype=dt, device=dev) if Lg > 0 else None,
+                dv=torch.empty(1, Lg, Hkv, D, dtype=dt, device=dev) if Lg > 0 else None,
+                delta=torch.empty(Hq * S, dtype=torch.float32, device=dev))
+
+
 def attn_bwd(q, k, v, o, lse, dout, code, bm: dict, P: int, scale: float, grad_start: int,
-             need_dq: bool = True):
+             passes: int = _lib.BWD_DQ | _lib.BWD_DKDV, buffers: dict | None = None):
     """Gradients of ``attn_fwd``. Returns dq [1, Hq, S, D] (a transposed view of
     an [1, S, Hq, D] buffer), and dk, dv [1, Hkv, L - grad_start, D] (views of
-    [1, L - grad_start, Hkv, D] buffers) or None when grad_start == L."""
+    [1, L - grad_start, Hkv, D] buffers) or None when grad_start == L.
+
+    ``passes`` selects the dQ pass (which also writes delta = rowsum(o * dout))
+    and/or the dK/dV pass; to issue them as two calls in stream order, pass the
+    same ``buffers`` (from ``bwd_buffers``) to both, the dQ pass first."""
     qq, q_sh, q_ss = _rows("query", q)
     kk, k_sh, k_ss = _rows("key", k)
     vv, v_sh, v_ss = _rows("value", v)
@@ -195,17 +212,12 @@ def attn_bwd(q, k, v, o, lse, dout, code, bm: dict, P: int, scale: float, grad_s
     if d3.stride(2) != 1 or (d3.stride(0) * d3.element_size()) % 16 or (d3.stride(1) * d3.element_size()) % 16 \
             or d3.data_ptr() % 16:
         d3 = d3.contiguous()
-    dev = qq.device
-    dq = torch.empty(1, S, Hq, D, dtype=qq.dtype, device=dev)
-    Lg = L - grad_start
-    if Lg > 0:
-        dk = torch.empty(1, Lg, Hkv, D, dtype=qq.dtype, device=dev)
-        dv = torch.empty(1, Lg, Hkv, D, dtype=qq.dtype, device=dev)
-        dk_ptr, dv_ptr = dk.data_ptr(), dv.data_ptr()
-    else:
-        dk = dv = None
-        dk_ptr = dv_ptr = None
-    delta = torch.empty(Hq * S, dtype=torch.float32, device=dev)
+    b = buffers if buffers is not None else bwd_buffers(q, k, grad_start)
+    dq, dk, dv, delta = b["dq"], b["dk"], b["dv"], b["delta"]
+    if dq.shape != (1, S, Hq, D) or delta.numel() != Hq * S:
+        raise ValueError("backward buffers do not match the operands")
+    dk_ptr = dk.data_ptr() if dk is not None else None
+    dv_ptr = dv.data_ptr() if dv is not None else None
     # o3 is [S, Hq, D]: element (h, s, d) at h * D + s * Hq * D + d
     _lib.call("mga_attn_bwd", qq.data_ptr(), q_sh, q_ss, kk.data_ptr(), k_sh, k_ss,
               vv.data_ptr(), v_sh, v_ss, o3.data_ptr(), o3.stride(1), o3.stride(0),
@@ -216,7 +228,7 @@ def attn_bwd(q, k, v, o, lse, dout, code, bm: dict, P: int, scale: float, grad_s
               bm["full_kv_num_blocks"].data_ptr(), bm["full_kv_indices"].data_ptr(),
               bm["q_num_blocks"].data_ptr(), bm["q_indices"].data_ptr(),
               bm["full_q_num_blocks"].data_ptr(), bm["full_q_indices"].data_ptr(),
-              S, L, P, Hq, Hkv, D, dtype_code(qq.dtype), float(scale), _stream(qq))
+              S, L, P, Hq, Hkv, D, dtype_code(qq.dtype), float(scale), int(passes), _stream(qq))
     dq_t = dq.transpose(1, 2)
     if dk is None:
         return dq_t, None, None
