@@ -1,4 +1,4 @@
-// MTP block-masked GQA attention, forward and backward, for gfx950.
+// MTP block-masked GQA attention backward for gfx950 (the forward is in mga_fwd.hip).
 //
 // Arithmetic: bf16 operands on v_mfma_f32_32x32x16_bf16, fp32 accumulation,
 // softmax in the log2 domain (exp2 of scale*log2(e)*q.k). Semantics follow the
@@ -67,174 +67,6 @@ __device__ __forceinline__ void stage_rows_t(bf16_t *dst, const T *src, int64_t 
       bf16x4 col;
       col[0] = rows[0][e]; col[1] = rows[1][e]; col[2] = rows[2][e]; col[3] = rows[3][e];
       *reinterpret_cast<i32x2 *>(dst + (dg * 8 + e) * ROW + kg * 4) = __builtin_bit_cast(i32x2, col);
-    }
-  }
-}
-
-// ---------------------------------------------------------------------------
-// Forward. One workgroup = one 128-row query tile of one query head, two
-// waves of 64 rows each. K and V^T are staged through LDS 64 keys at a time.
-// ---------------------------------------------------------------------------
-template <int HD, typename T>
-__global__ __launch_bounds__(128) void attn_fwd_kernel(AttnArgs a) {
-  constexpr int BK = 64;
-  constexpr int KS = HD / 16;
-  constexpr int DB = HD / 32;
-  constexpr int KROW = HD + 8;
-  constexpr int VROW = BK + 4;
-  constexpr int NT = 128;
-  __shared__ __attribute__((aligned(16))) bf16_t sK[BK * KROW];
-  __shared__ __attribute__((aligned(16))) bf16_t sVt[HD * VROW];
-  __shared__ __attribute__((aligned(16))) int sKc[BK];
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int l32 = lane & 31, hi = lane >> 5;
-  const int G = a.Hq / a.Hkv;
-  // logical order (kv head, query tile descending, head in group); consecutive
-  // logical indices share an XCD so the G heads of a group share its L2.
-  const int li = xcd_swizzle(blockIdx.x, a.nQ * a.Hq);
-  const int hh = li % G;
-  const int rest = li / G;
-  const int qt = a.nQ - 1 - rest % a.nQ;
-  const int g = rest / a.nQ;
-  const int h = g * G + hh;
-
-  const T *qp = reinterpret_cast<const T *>(a.q) + h * a.q_sh;
-  const T *kp = reinterpret_cast<const T *>(a.k) + g * a.k_sh;
-  const T *vp = reinterpret_cast<const T *>(a.v) + g * a.v_sh;
-
-  bf16x8 qf[2][KS];
-  int qrow[2], qcode[2];
-#pragma unroll
-  for (int nb = 0; nb < 2; ++nb) {
-    qrow[nb] = qt * kBlock + wave * 64 + nb * 32 + l32;
-    const int qr = min(qrow[nb], a.S - 1);
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) qf[nb][ks] = load8(qp + (int64_t)qr * a.q_ss + ks * 16 + hi * 8);
-    qcode[nb] = qrow[nb] < a.S ? a.code[qrow[nb]] : kCodePad;
-  }
-
-  float m_run[2] = {kNegInf, kNegInf};
-  float l_run[2] = {0.f, 0.f};
-  f32x16 oacc[2][DB];
-#pragma unroll
-  for (int nb = 0; nb < 2; ++nb)
-#pragma unroll
-    for (int db = 0; db < DB; ++db) oacc[nb][db] = zero16();
-
-  const int npart = a.kv_num[qt];
-  const int ntot = npart + a.fkv_num[qt];
-  const int32_t *pidx = a.kv_idx + (int64_t)qt * a.nKV;
-  const int32_t *fidx = a.fkv_idx + (int64_t)qt * a.nKV;
-
-  for (int it = 0; it < ntot; ++it) {
-    const bool partial = it < npart;
-    const int kt = partial ? pidx[it] : fidx[it - npart];
-    for (int sub = 0; sub < kBlock / BK; ++sub) {
-      const int kbase = kt * kBlock + sub * BK;
-      if (kbase >= a.L) break;
-      __syncthreads();
-      stage_rows<HD, BK, KROW, NT>(sK, kp, a.k_ss, kbase, a.L - 1);
-      stage_rows_t<HD, BK, VROW, NT>(sVt, vp, a.v_ss, kbase, a.L - 1);
-      if (tid < BK) sKc[tid] = key_code(a.code, kbase + tid, a.P, a.L);
-      __syncthreads();
-
-      f32x16 sacc[2][2];
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int nb = 0; nb < 2; ++nb) sacc[kb][nb] = zero16();
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-          const bf16x8 af = lds_read8(sK + (kb * 32 + l32) * KROW + ks * 16 + hi * 8);
-#pragma unroll
-          for (int nb = 0; nb < 2; ++nb) sacc[kb][nb] = mfma32(af, qf[nb][ks], sacc[kb][nb]);
-        }
-      }
-
-#pragma unroll
-      for (int nb = 0; nb < 2; ++nb) {
-        float mx = kNegInf;
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int kl0 = kb * 32 + 8 * i + 4 * hi;
-            const i32x4 kc = *reinterpret_cast<const i32x4 *>(sKc + kl0);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              float s = sacc[kb][nb][4 * i + j] * a.scale_log2;
-              if (partial && !mtp_allowed(qrow[nb] + a.P, qcode[nb], kbase + kl0 + j, kc[j])) s = kNegInf;
-              sacc[kb][nb][4 * i + j] = s;
-              mx = fmaxf(mx, s);
-            }
-          }
-        }
-        mx = fmaxf(mx, xor32(mx));
-        const float m_new = fmaxf(m_run[nb], mx);
-        const float m_use = m_new == kNegInf ? 0.f : m_new;
-        const float alpha = fast_exp2(m_run[nb] - m_use);
-        float ps = 0.f;
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const float p = fast_exp2(sacc[kb][nb][r] - m_use);
-            sacc[kb][nb][r] = p;
-            ps += p;
-          }
-        l_run[nb] = l_run[nb] * alpha + ps;
-        m_run[nb] = m_new;
-#pragma unroll
-        for (int db = 0; db < DB; ++db)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) oacc[nb][db][r] *= alpha;
-      }
-
-      bf16x8 pb[2][2][2];
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int nb = 0; nb < 2; ++nb)
-#pragma unroll
-          for (int u = 0; u < 2; ++u) {
-            const f32x16 &s = sacc[kb][nb];
-            pb[kb][nb][u] = pack8(s[8 * u + 0], s[8 * u + 1], s[8 * u + 2], s[8 * u + 3],
-                                  s[8 * u + 4], s[8 * u + 5], s[8 * u + 6], s[8 * u + 7]);
-          }
-#pragma unroll
-      for (int db = 0; db < DB; ++db)
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int u = 0; u < 2; ++u) {
-            const bf16_t *vr = sVt + (db * 32 + l32) * VROW + kb * 32 + 16 * u + 4 * hi;
-            const bf16x8 af = lds_read4x2(vr, vr + 8);
-#pragma unroll
-            for (int nb = 0; nb < 2; ++nb) oacc[nb][db] = mfma32(af, pb[kb][nb][u], oacc[nb][db]);
-          }
-    }
-  }
-
-  T *op = reinterpret_cast<T *>(const_cast<void *>(a.o)) + h * a.o_sh;
-#pragma unroll
-  for (int nb = 0; nb < 2; ++nb) {
-    const float lt = l_run[nb] + xor32(l_run[nb]);
-    const float inv = lt > 0.f ? 1.f / lt : 0.f;
-    if (qrow[nb] < a.S) {
-      if (hi == 0)
-        a.lse[(int64_t)h * a.S + qrow[nb]] = lt > 0.f ? (m_run[nb] + __log2f(lt)) * kLn2 : kNegInf;
-      T *orow = op + (int64_t)qrow[nb] * a.o_ss;
-#pragma unroll
-      for (int db = 0; db < DB; ++db)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const f32x16 &c = oacc[nb][db];
-          store4(orow + db * 32 + 8 * i + 4 * hi, c[4 * i] * inv, c[4 * i + 1] * inv,
-                 c[4 * i + 2] * inv, c[4 * i + 3] * inv);
-        }
     }
   }
 }
@@ -561,11 +393,6 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a, int kt0,
 // Launchers
 // ---------------------------------------------------------------------------
 template <int HD, typename T>
-static void fwd_impl(const AttnArgs &a, hipStream_t st) {
-  hipLaunchKernelGGL((attn_fwd_kernel<HD, T>), dim3(a.nQ * a.Hq), dim3(128), 0, st, a);
-}
-
-template <int HD, typename T>
 static void bwd_impl(const AttnArgs &a, int passes, hipStream_t st) {
   constexpr int RPB = 256 / (HD / 8);
   const int rows = a.S * a.Hq;
@@ -577,14 +404,6 @@ static void bwd_impl(const AttnArgs &a, int passes, hipStream_t st) {
   const int nkt = a.nKV - kt0;
   if ((passes & kBwdDkDv) && nkt > 0 && a.grad_start < a.L)
     hipLaunchKernelGGL((attn_bwd_dkdv_kernel<HD, T>), dim3(nkt * a.Hkv), dim3(256), 0, st, a, kt0, nkt);
-}
-
-void launch_attn_fwd(const AttnArgs &a, int head_dim, bool is_f32, hipStream_t st) {
-  if (head_dim == 128) {
-    if (is_f32) fwd_impl<128, float>(a, st); else fwd_impl<128, bf16_t>(a, st);
-  } else {
-    if (is_f32) fwd_impl<64, float>(a, st); else fwd_impl<64, bf16_t>(a, st);
-  }
 }
 
 void launch_attn_bwd(const AttnArgs &a, int head_dim, bool is_f32, int passes, hipStream_t st) {

@@ -106,3 +106,107 @@ __device__ __forceinline__ int xcd_swizzle(int b, int n) {
 }
 
 }  // namespace mga
+
+namespace mga {
+
+// ---- LDS tiles: rows of HD bf16, 16-byte granules XOR-swizzled per row -----
+// Granule c of row r sits at slot c ^ swz(r). The map (linear over GF(2) in
+// the low four row bits) keeps both access patterns the kernels use free of
+// bank conflicts for 32- and 64-bank LDS: 16-byte row reads of one granule
+// by 16 consecutive rows, and the 8-byte transpose reads of 4 consecutive rows
+// x 16 (or 32) consecutive columns.
+template <int HD>
+__device__ __forceinline__ int swz(int r) {
+  if constexpr (HD == 128)
+    return ((r & 1) ? 4 : 0) ^ ((r & 2) ? 10 : 0) ^ ((r & 4) ? 1 : 0) ^ ((r & 8) ? 2 : 0);
+  else
+    return ((r & 1) ? 2 : 0) ^ ((r & 2) ? 4 : 0) ^ ((r & 4) ? 1 : 0) ^ ((r & 8) ? 2 : 0);
+}
+
+// Element offset of granule g (8 elements) of row r in a swizzled tile.
+template <int HD>
+__device__ __forceinline__ int tile_off(int r, int g) {
+  return r * HD + ((g ^ swz<HD>(r)) << 3);
+}
+
+typedef __attribute__((__vector_size__(4 * sizeof(short)))) short i16x4;
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+
+// 8-byte transpose read (ds_read_b64_tr_b16). Within each 16-lane group, lane
+// i receives element i % 4 of the 8-byte loads addressed by lanes i / 4 + 4k,
+// k = 0..3: pointing lane j at X[k0 + j / 4][m0 + 4 (j % 4)] of a row-major
+// tile hands lane i the column m0 + i at rows k0 .. k0 + 3.
+__device__ __forceinline__ i16x4 lds_tr4(const bf16_t *p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(p));
+}
+
+__device__ __forceinline__ bf16x8 join8(i16x4 a, i16x4 b) {
+  const i32x2 x = __builtin_bit_cast(i32x2, a), y = __builtin_bit_cast(i32x2, b);
+  i32x4 r = {x[0], x[1], y[0], y[1]};
+  return __builtin_bit_cast(bf16x8, r);
+}
+
+// Per-lane constants of a transposed MFMA A-operand read (32 m-rows x 16 k)
+// from a k-major swizzled tile: lane (l32, hi) needs column m0 + l32 at rows
+// k0 + 4 hi + 0..3 (slots 0..3) and k0 + 8 + 4 hi + 0..3 (slots 4..7), the k
+// order of a 32x32 accumulator's registers 8u .. 8u + 7. For k0 a multiple of
+// 16 and m0 a multiple of 32 the swizzle term only depends on the lane, so the
+// address is rowbase(k0) + lo[s] + ((m0 / 32) ^ hi2[s]) * 32.
+struct TrLane {
+  int row[2];   // tile row offset (in rows) of the two reads, relative to k0
+  int lo[2];    // low column part, elements
+  int hi2[2];   // XOR applied to the 32-column block index
+};
+
+template <int HD>
+__device__ __forceinline__ TrLane tr_lane(int lane) {
+  TrLane t;
+  const int i = lane & 15, hi = lane >> 5;
+  const int m = 16 * ((lane >> 4) & 1) + 4 * (i & 3);   // column within the 32-block
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    const int r = 4 * hi + (i >> 2) + 8 * s;
+    const int sw = swz<HD>(r);
+    t.row[s] = r;
+    t.lo[s] = ((((m >> 3) ^ sw) & 3) << 3) + (m & 7);
+    t.hi2[s] = sw >> 2;
+  }
+  return t;
+}
+
+template <int HD>
+__device__ __forceinline__ bf16x8 lds_tr_operand(const bf16_t *tile, const TrLane &t, int k0, int mblk) {
+  const bf16_t *p0 = tile + (k0 + t.row[0]) * HD + t.lo[0] + ((mblk ^ t.hi2[0]) << 5);
+  const bf16_t *p1 = tile + (k0 + t.row[1]) * HD + t.lo[1] + ((mblk ^ t.hi2[1]) << 5);
+  return join8(lds_tr4(p0), lds_tr4(p1));
+}
+
+// ---- global -> register -> LDS staging of an NR x HD tile ------------------
+// 256 threads; thread t owns granules t, t + 256, ...; rows beyond rmax repeat
+// row rmax (their values are masked or unused).
+template <int HD, int NR, typename T>
+struct TileStage {
+  static constexpr int kGran = NR * HD / 8 / 256;
+  i32x4 reg[kGran];
+
+  __device__ __forceinline__ void load(const T *src, int64_t ss, int r0, int rmax) {
+#pragma unroll
+    for (int i = 0; i < kGran; ++i) {
+      const int gi = threadIdx.x + 256 * i;
+      const int r = gi / (HD / 8), c = gi % (HD / 8);
+      const int row = min(r0 + r, rmax);
+      reg[i] = __builtin_bit_cast(i32x4, load8(src + (int64_t)row * ss + c * 8));
+    }
+  }
+
+  __device__ __forceinline__ void store(bf16_t *tile) const {
+#pragma unroll
+    for (int i = 0; i < kGran; ++i) {
+      const int gi = threadIdx.x + 256 * i;
+      const int r = gi / (HD / 8), c = gi % (HD / 8);
+      *reinterpret_cast<i32x4 *>(tile + tile_off<HD>(r, c)) = reg[i];
+    }
+  }
+};
+
+}  // namespace mga

@@ -1,0 +1,246 @@
+// MTP block-masked GQA attention forward for gfx950.
+//
+// Work item = (kv head g, slice of the G query heads, block of query rows).
+// A workgroup of 4 waves holds 4 (query head, 32-row block) pairs of one kv
+// head: with G a multiple of 4 that is 4 heads x the same 32 rows, so every
+// K/V tile staged in LDS feeds four heads. Each wave computes
+//   S^T = K Q^T  (v_mfma_f32_32x32x16_bf16; lane = query column)
+// over 64-key steps, keeps the online-softmax state of its query in the lane
+// (plus one exchange with the lane 32 away) and accumulates O^T += V^T P^T,
+// feeding the probabilities from the accumulator registers straight into the
+// B operand. V^T comes from the row-major V tile through the LDS transpose
+// read. K/V tiles are prefetched into registers one step ahead and written
+// to a second LDS buffer, so one barrier per step suffices.
+//
+// Rescaling of O is lazy: the running max only moves when a new score exceeds
+// it by more than 2^8 (log2 domain), which keeps every probability below 256
+// and leaves the result exact up to rounding (the final normalisation uses the
+// same max). Semantics: [torch]_higher_order_ops/flex_attention.py:202-267
+// (masked scores are -inf; a fully masked row has output 0 and LSE -inf).
+#include "mga_common.hpp"
+#include "mga_internal.hpp"
+
+namespace mga {
+
+namespace {
+
+constexpr float kNegInfF = -__builtin_huge_valf();
+constexpr float kLazyMax = 8.0f;   // log2-domain slack before O is rescaled
+constexpr int kStepKeys = 64;
+
+__device__ __forceinline__ float exp2f_(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Heads sharing a workgroup (a divisor of both G and 4) and 32-row blocks per head.
+__host__ __device__ __forceinline__ int heads_per_wg(int G) { return (G % 4 == 0) ? 4 : (G % 2 == 0 ? 2 : 1); }
+
+}  // namespace
+
+template <int HD, typename T>
+__global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
+  constexpr int KS = HD / 16;          // k-steps of QK^T over head_dim
+  constexpr int DB = HD / 32;          // 32-dim blocks of O^T
+  constexpr int TILE = kStepKeys * HD; // elements of one K or V step tile
+  __shared__ __attribute__((aligned(16))) bf16_t sK[2][TILE];
+  __shared__ __attribute__((aligned(16))) bf16_t sV[2][TILE];
+  __shared__ __attribute__((aligned(16))) int sC[2][kStepKeys];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, hi = lane >> 5;
+  const int G = a.Hq / a.Hkv;
+  const int HPW = heads_per_wg(G);
+  const int RB = 4 / HPW;                 // 32-row blocks per head in this workgroup
+  const int QR = 32 * RB;                 // query rows per workgroup
+  const int nslice = G / HPW;
+  const int nqb = (a.S + QR - 1) / QR;
+
+  // logical item: kv head major (one kv head per XCD when Hkv = 8), then query
+  // blocks from the last (longest) to the first, then the head slice
+  const int li = xcd_swizzle(blockIdx.x, a.Hkv * nslice * nqb);
+  const int g = li / (nslice * nqb);
+  const int rem = li % (nslice * nqb);
+  const int qb = nqb - 1 - rem / nslice;
+  const int slice = rem % nslice;
+  const int h = g * G + slice * HPW + wave % HPW;
+  const int row = qb * QR + (wave / HPW) * 32 + l32;   // this lane's query row
+  const int qt = (qb * QR) / kBlock;                   // block-mask query tile
+
+  const T *qp = reinterpret_cast<const T *>(a.q) + h * a.q_sh;
+  const T *kp = reinterpret_cast<const T *>(a.k) + g * a.k_sh;
+  const T *vp = reinterpret_cast<const T *>(a.v) + g * a.v_sh;
+
+  bf16x8 qf[KS];
+  {
+    const int qr = min(row, a.S - 1);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) qf[ks] = load8(qp + (int64_t)qr * a.q_ss + ks * 16 + hi * 8);
+  }
+  const int qcode = row < a.S ? a.code[row] : kCodePad;
+  // a pad query (or a row past S) sees no key: fold that into the causal bound
+  const int qlim = (qcode == kCodePad) ? -1 : row + a.P;
+
+  const int npart = a.kv_num[qt];
+  const int ntot = npart + a.fkv_num[qt];
+  const int32_t *pidx = a.kv_idx + (int64_t)qt * a.nKV;
+  const int32_t *fidx = a.fkv_idx + (int64_t)qt * a.nKV;
+  const int nstep = 2 * ntot;
+  auto step_base = [&](int j) {
+    const int it = j >> 1;
+    const int kt = it < npart ? pidx[it] : fidx[it - npart];
+    return kt * kBlock + (j & 1) * kStepKeys;
+  };
+
+  // per-lane LDS offsets: K rows (A operand of QK^T) and the V^T transpose reads
+  const int krow_sw = swz<HD>(l32);
+  const TrLane tl = tr_lane<HD>(lane);
+
+  TileStage<HD, kStepKeys, T> stK, stV;
+  int creg = 0;
+  auto load_step = [&](int j) {
+    const int kb = step_base(j);
+    stK.load(kp, a.k_ss, kb, a.L - 1);
+    stV.load(vp, a.v_ss, kb, a.L - 1);
+    if (tid < kStepKeys) creg = key_code(a.code, kb + tid, a.P, a.L);
+  };
+  auto store_step = [&](int buf) {
+    stK.store(sK[buf]);
+    stV.store(sV[buf]);
+    if (tid < kStepKeys) sC[buf][tid] = creg;
+  };
+
+  float m_run = kNegInfF, m_use = 0.f, l_run = 0.f;
+  f32x16 oacc[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) oacc[db] = zero16();
+
+  if (nstep > 0) {
+    load_step(0);
+    store_step(0);
+  }
+  __syncthreads();
+
+  for (int j = 0; j < nstep; ++j) {
+    const int buf = j & 1;
+    const int kbase = step_base(j);
+    const bool partial = (j >> 1) < npart;
+    if (j + 1 < nstep) load_step(j + 1);
+
+    if (kbase < a.L) {
+      const bf16_t *tK = sK[buf];
+      const bf16_t *tV = sV[buf];
+      // ---- S^T = K Q^T for 64 keys x 32 queries -----------------------------
+      f32x16 sacc[2] = {zero16(), zero16()};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+          const int r = kb * 32 + l32;
+          const bf16x8 af = lds_read8(tK + r * HD + (((2 * ks + hi) ^ krow_sw) << 3));
+          sacc[kb] = mfma32(af, qf[ks], sacc[kb]);
+        }
+      }
+      // ---- mask, running max -------------------------------------------------
+      float mx = kNegInfF;
+      if (partial) {
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int kl0 = kb * 32 + 8 * i + 4 * hi;
+            const i32x4 kc = *reinterpret_cast<const i32x4 *>(&sC[buf][kl0]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const bool ok = (kbase + kl0 + e <= qlim) & ((kc[e] == kCodeX) | (kc[e] == qcode));
+              const float s = ok ? sacc[kb][4 * i + e] : kNegInfF;
+              sacc[kb][4 * i + e] = s;
+              mx = fmaxf(mx, s);
+            }
+          }
+      } else {
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kb][r]);
+      }
+      mx = fmaxf(mx, xor32(mx)) * a.scale_log2;
+      const bool need = mx > m_run + kLazyMax;
+      if (__builtin_amdgcn_ballot_w64(need)) {
+        const float m_new = fmaxf(m_run, mx);
+        const float alpha = exp2f_(m_run - m_new);     // 0 when m_run = -inf
+        if (m_new != m_run) {
+          l_run *= alpha;
+#pragma unroll
+          for (int db = 0; db < DB; ++db)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
+        }
+        m_run = m_new;
+        m_use = m_run == kNegInfF ? 0.f : m_run;
+      }
+      // ---- P = exp2(s * scale_log2 - m) ----------------------------------------
+      float ps = 0.f;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float p = exp2f_(__builtin_fmaf(sacc[kb][r], a.scale_log2, -m_use));
+          sacc[kb][r] = p;
+          ps += p;
+        }
+      l_run += ps;
+      // ---- O^T += V^T P^T ------------------------------------------------------
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const f32x16 &s = sacc[kb];
+          const bf16x8 pb = pack8(s[8 * u + 0], s[8 * u + 1], s[8 * u + 2], s[8 * u + 3],
+                                  s[8 * u + 4], s[8 * u + 5], s[8 * u + 6], s[8 * u + 7]);
+#pragma unroll
+          for (int db = 0; db < DB; ++db) {
+            const bf16x8 af = lds_tr_operand<HD>(tV, tl, kb * 32 + 16 * u, db);
+            oacc[db] = mfma32(af, pb, oacc[db]);
+          }
+        }
+    }
+
+    if (j + 1 < nstep) store_step(buf ^ 1);
+    __syncthreads();
+  }
+
+  // ---- epilogue: normalise, write O [S, Hq, D] and the natural-log LSE -------
+  const float lt = l_run + xor32(l_run);
+  if (row < a.S) {
+    const float inv = lt > 0.f ? 1.f / lt : 0.f;
+    if (hi == 0)
+      a.lse[(int64_t)h * a.S + row] = lt > 0.f ? (m_run + __log2f(lt)) * kLn2 : kNegInfF;
+    T *orow = reinterpret_cast<T *>(const_cast<void *>(a.o)) + h * a.o_sh + (int64_t)row * a.o_ss;
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const f32x16 &c = oacc[db];
+        store4(orow + db * 32 + 8 * i + 4 * hi, c[4 * i] * inv, c[4 * i + 1] * inv,
+               c[4 * i + 2] * inv, c[4 * i + 3] * inv);
+      }
+  }
+}
+
+template <int HD, typename T>
+static void fwd_launch(const AttnArgs &a, hipStream_t st) {
+  const int G = a.Hq / a.Hkv;
+  const int HPW = heads_per_wg(G);
+  const int QR = 32 * (4 / HPW);
+  const int nqb = (a.S + QR - 1) / QR;
+  const int items = a.Hkv * (G / HPW) * nqb;
+  hipLaunchKernelGGL((attn_fwd_kernel<HD, T>), dim3(items), dim3(256), 0, st, a);
+}
+
+void launch_attn_fwd(const AttnArgs &a, int head_dim, bool is_f32, hipStream_t st) {
+  if (head_dim == 128) {
+    if (is_f32) fwd_launch<128, float>(a, st); else fwd_launch<128, bf16_t>(a, st);
+  } else {
+    if (is_f32) fwd_launch<64, float>(a, st); else fwd_launch<64, bf16_t>(a, st);
+  }
+}
+
+}  // namespace mga
