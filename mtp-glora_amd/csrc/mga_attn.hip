@@ -72,185 +72,6 @@ __device__ __forceinline__ void stage_rows_t(bf16_t *dst, const T *src, int64_t 
 }
 
 // ---------------------------------------------------------------------------
-// Backward prologue: delta[h, s] = sum_d o[s, h, d] * dout[s, h, d] (fp32).
-// ---------------------------------------------------------------------------
-template <int HD, typename T>
-__global__ __launch_bounds__(256) void attn_bwd_delta_kernel(AttnArgs a) {
-  constexpr int TPR = HD / 8;           // threads per row
-  constexpr int RPB = 256 / TPR;        // rows per block
-  const int rr = blockIdx.x * RPB + threadIdx.x / TPR;
-  const int c = (threadIdx.x % TPR) * 8;
-  float acc = 0.f;
-  const int nrows = a.S * a.Hq;
-  if (rr < nrows) {
-    const int s = rr / a.Hq, h = rr % a.Hq;
-    const bf16x8 o = load8(reinterpret_cast<const T *>(a.o) + h * a.o_sh + (int64_t)s * a.o_ss + c);
-    const bf16x8 d = load8(reinterpret_cast<const T *>(a.dout) + h * a.do_sh + (int64_t)s * a.do_ss + c);
-    if constexpr (sizeof(T) == 2) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc += (float)o[e] * (float)d[e];
-    }
-  }
-  if constexpr (sizeof(T) == 4) {
-    // fp32 operands: accumulate from the original values, not the bf16 copies
-    if (rr < nrows) {
-      const int s = rr / a.Hq, h = rr % a.Hq;
-      const float *o = reinterpret_cast<const float *>(a.o) + h * a.o_sh + (int64_t)s * a.o_ss + c;
-      const float *d = reinterpret_cast<const float *>(a.dout) + h * a.do_sh + (int64_t)s * a.do_ss + c;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc += o[e] * d[e];
-    }
-  }
-#pragma unroll
-  for (int off = TPR / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
-  if (rr < nrows && (threadIdx.x % TPR) == 0) {
-    const int s = rr / a.Hq, h = rr % a.Hq;
-    a.delta[(int64_t)h * a.S + s] = acc;
-  }
-}
-
-// ---------------------------------------------------------------------------
-// Backward dQ pass. Same workgroup shape as the forward; K, K^T and V are
-// staged 32 keys at a time. Per key block:
-//   S^T = K Q^T, dP^T = V dO^T, P^T = exp2(S^T*c - lse2), dS^T = P^T (dP^T - delta),
-//   dQ^T += K^T dS^T.
-// ---------------------------------------------------------------------------
-template <int HD, typename T>
-__global__ __launch_bounds__(128) void attn_bwd_dq_kernel(AttnArgs a) {
-  constexpr int BK = 32;
-  constexpr int KS = HD / 16;
-  constexpr int DB = HD / 32;
-  constexpr int KROW = HD + 8;
-  constexpr int TROW = BK + 4;
-  constexpr int NT = 128;
-  __shared__ __attribute__((aligned(16))) bf16_t sK[BK * KROW];
-  __shared__ __attribute__((aligned(16))) bf16_t sV[BK * KROW];
-  __shared__ __attribute__((aligned(16))) bf16_t sKt[HD * TROW];
-  __shared__ __attribute__((aligned(16))) int sKc[BK];
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int l32 = lane & 31, hi = lane >> 5;
-  const int G = a.Hq / a.Hkv;
-  const int li = xcd_swizzle(blockIdx.x, a.nQ * a.Hq);
-  const int hh = li % G;
-  const int rest = li / G;
-  const int qt = a.nQ - 1 - rest % a.nQ;
-  const int g = rest / a.nQ;
-  const int h = g * G + hh;
-
-  const T *qp = reinterpret_cast<const T *>(a.q) + h * a.q_sh;
-  const T *dop = reinterpret_cast<const T *>(a.dout) + h * a.do_sh;
-  const T *kp = reinterpret_cast<const T *>(a.k) + g * a.k_sh;
-  const T *vp = reinterpret_cast<const T *>(a.v) + g * a.v_sh;
-
-  bf16x8 qf[2][KS], df[2][KS];
-  int qrow[2], qcode[2];
-  float lse2[2], del[2];
-#pragma unroll
-  for (int nb = 0; nb < 2; ++nb) {
-    qrow[nb] = qt * kBlock + wave * 64 + nb * 32 + l32;
-    const int qr = min(qrow[nb], a.S - 1);
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      qf[nb][ks] = load8(qp + (int64_t)qr * a.q_ss + ks * 16 + hi * 8);
-      df[nb][ks] = load8(dop + (int64_t)qr * a.do_ss + ks * 16 + hi * 8);
-    }
-    const bool in = qrow[nb] < a.S;
-    qcode[nb] = in ? a.code[qrow[nb]] : kCodePad;
-    lse2[nb] = in ? a.lse[(int64_t)h * a.S + qrow[nb]] * kLog2e : 0.f;
-    del[nb] = in ? a.delta[(int64_t)h * a.S + qrow[nb]] : 0.f;
-  }
-
-  f32x16 dqacc[2][DB];
-#pragma unroll
-  for (int nb = 0; nb < 2; ++nb)
-#pragma unroll
-    for (int db = 0; db < DB; ++db) dqacc[nb][db] = zero16();
-
-  const int npart = a.kv_num[qt];
-  const int ntot = npart + a.fkv_num[qt];
-  const int32_t *pidx = a.kv_idx + (int64_t)qt * a.nKV;
-  const int32_t *fidx = a.fkv_idx + (int64_t)qt * a.nKV;
-
-  for (int it = 0; it < ntot; ++it) {
-    const bool partial = it < npart;
-    const int kt = partial ? pidx[it] : fidx[it - npart];
-    for (int sub = 0; sub < kBlock / BK; ++sub) {
-      const int kbase = kt * kBlock + sub * BK;
-      if (kbase >= a.L) break;
-      __syncthreads();
-      stage_rows<HD, BK, KROW, NT>(sK, kp, a.k_ss, kbase, a.L - 1);
-      stage_rows<HD, BK, KROW, NT>(sV, vp, a.v_ss, kbase, a.L - 1);
-      stage_rows_t<HD, BK, TROW, NT>(sKt, kp, a.k_ss, kbase, a.L - 1);
-      if (tid < BK) sKc[tid] = key_code(a.code, kbase + tid, a.P, a.L);
-      __syncthreads();
-
-      f32x16 sacc[2], dpacc[2];
-#pragma unroll
-      for (int nb = 0; nb < 2; ++nb) { sacc[nb] = zero16(); dpacc[nb] = zero16(); }
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        const bf16x8 ak = lds_read8(sK + l32 * KROW + ks * 16 + hi * 8);
-        const bf16x8 av = lds_read8(sV + l32 * KROW + ks * 16 + hi * 8);
-#pragma unroll
-        for (int nb = 0; nb < 2; ++nb) {
-          sacc[nb] = mfma32(ak, qf[nb][ks], sacc[nb]);
-          dpacc[nb] = mfma32(av, df[nb][ks], dpacc[nb]);
-        }
-      }
-#pragma unroll
-      for (int nb = 0; nb < 2; ++nb) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int kl0 = 8 * i + 4 * hi;
-          const i32x4 kc = *reinterpret_cast<const i32x4 *>(sKc + kl0);
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const int r = 4 * i + j;
-            float p = fast_exp2(sacc[nb][r] * a.scale_log2 - lse2[nb]);
-            if (partial && !mtp_allowed(qrow[nb] + a.P, qcode[nb], kbase + kl0 + j, kc[j])) p = 0.f;
-            dpacc[nb][r] = p * (dpacc[nb][r] - del[nb]);
-          }
-        }
-      }
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        bf16x8 dsb[2];
-#pragma unroll
-        for (int nb = 0; nb < 2; ++nb) {
-          const f32x16 &d = dpacc[nb];
-          dsb[nb] = pack8(d[8 * u + 0], d[8 * u + 1], d[8 * u + 2], d[8 * u + 3], d[8 * u + 4],
-                          d[8 * u + 5], d[8 * u + 6], d[8 * u + 7]);
-        }
-#pragma unroll
-        for (int db = 0; db < DB; ++db) {
-          const bf16_t *kr = sKt + (db * 32 + l32) * TROW + 16 * u + 4 * hi;
-          const bf16x8 af = lds_read4x2(kr, kr + 8);
-#pragma unroll
-          for (int nb = 0; nb < 2; ++nb) dqacc[nb][db] = mfma32(af, dsb[nb], dqacc[nb][db]);
-        }
-      }
-    }
-  }
-
-  T *dqp = reinterpret_cast<T *>(a.dq) + h * a.dq_sh;
-#pragma unroll
-  for (int nb = 0; nb < 2; ++nb) {
-    if (qrow[nb] < a.S) {
-      T *row = dqp + (int64_t)qrow[nb] * a.dq_ss;
-#pragma unroll
-      for (int db = 0; db < DB; ++db)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const f32x16 &c = dqacc[nb][db];
-          store4(row + db * 32 + 8 * i + 4 * hi, c[4 * i] * a.scale, c[4 * i + 1] * a.scale,
-                 c[4 * i + 2] * a.scale, c[4 * i + 3] * a.scale);
-        }
-    }
-  }
-}
-
-// ---------------------------------------------------------------------------
 // Backward dK/dV pass over the key tiles that receive gradient (keys >=
 // grad_start). One workgroup = one 128-key tile of one kv head, four waves of
 // 32 keys; the G query heads of the group are reduced inside the workgroup.
@@ -393,13 +214,11 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a, int kt0,
 // Launchers
 // ---------------------------------------------------------------------------
 template <int HD, typename T>
+void dq_launch(const AttnArgs &a, hipStream_t st);   // mga_bwd_dq.hip
+
+template <int HD, typename T>
 static void bwd_impl(const AttnArgs &a, int passes, hipStream_t st) {
-  constexpr int RPB = 256 / (HD / 8);
-  const int rows = a.S * a.Hq;
-  if (passes & kBwdDq) {
-    hipLaunchKernelGGL((attn_bwd_delta_kernel<HD, T>), dim3((rows + RPB - 1) / RPB), dim3(256), 0, st, a);
-    hipLaunchKernelGGL((attn_bwd_dq_kernel<HD, T>), dim3(a.nQ * a.Hq), dim3(128), 0, st, a);
-  }
+  if (passes & kBwdDq) dq_launch<HD, T>(a, st);
   const int kt0 = a.grad_start / kBlock;
   const int nkt = a.nKV - kt0;
   if ((passes & kBwdDkDv) && nkt > 0 && a.grad_start < a.L)

@@ -1,0 +1,238 @@
+// MTP block-masked GQA attention backward, dQ pass, for gfx950.
+//
+// Same work decomposition as the forward (mga_fwd.hip): a workgroup of 4 waves
+// holds 4 (query head, 32-row block) pairs of one kv head, so each staged K/V
+// tile feeds four heads. Per 64-key step each wave computes
+//   S^T  = K Q^T,  dP^T = V dO^T                    (A operands: K, V rows)
+//   P    = exp2(S^T * scale_log2 - lse_log2)         (0 where masked)
+//   dS^T = P (dP^T - delta)
+//   dQ^T += K^T dS^T                                  (A operand: K^T by transpose read)
+// and finally dQ = scale * dQ^T^T. The prologue forms delta = rowsum(O * dO)
+// for the wave's rows (fp32, from the stored operands) and writes it for the
+// dK/dV pass. Semantics: [torch]_higher_order_ops/flex_attention.py:826-990
+// with grad_lse = 0; a fully masked row (LSE -inf) gets dQ = 0.
+#include <type_traits>
+
+#include "mga_common.hpp"
+#include "mga_internal.hpp"
+
+namespace mga {
+
+namespace {
+
+constexpr float kNegInfD = -__builtin_huge_valf();
+constexpr int kStep = 64;
+
+__host__ __device__ __forceinline__ int heads_per_wg_dq(int G) { return (G % 4 == 0) ? 4 : (G % 2 == 0 ? 2 : 1); }
+
+// Sum over this lane's half of the row (dims ks*16 + hi*8 .. +8) of o * d.
+template <int HD, typename T>
+__device__ __forceinline__ float half_row_dot(const T *o, const T *d, int hi) {
+  float acc = 0.f;
+#pragma unroll
+  for (int ks = 0; ks < HD / 16; ++ks) {
+    const int c = ks * 16 + hi * 8;
+    if constexpr (sizeof(T) == 2) {
+      const bf16x8 x = load8(o + c), y = load8(d + c);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc += (float)x[e] * (float)y[e];
+    } else {
+      const f32x4 x0 = *reinterpret_cast<const f32x4 *>(o + c), x1 = *reinterpret_cast<const f32x4 *>(o + c + 4);
+      const f32x4 y0 = *reinterpret_cast<const f32x4 *>(d + c), y1 = *reinterpret_cast<const f32x4 *>(d + c + 4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc += x0[e] * y0[e] + x1[e] * y1[e];
+    }
+  }
+  return acc;
+}
+
+}  // namespace
+
+template <int HD, typename T>
+__global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnArgs a) {
+  constexpr int KS = HD / 16;
+  constexpr int DB = HD / 32;
+  constexpr int TILE = kStep * HD;
+  // two named buffers per operand (not one array of two): distinct LDS objects
+  // let the compiler see that the direct loads into one buffer never alias the
+  // reads of the other, so it does not wait for them before computing
+  __shared__ __attribute__((aligned(16))) bf16_t sK0[TILE], sK1[TILE];
+  __shared__ __attribute__((aligned(16))) bf16_t sV0[TILE], sV1[TILE];
+  __shared__ __attribute__((aligned(16))) int sC0[kStep], sC1[kStep];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, hi = lane >> 5;
+  const int G = a.Hq / a.Hkv;
+  const int HPW = heads_per_wg_dq(G);
+  const int QR = 32 * (4 / HPW);
+  const int nslice = G / HPW;
+  const int nqb = (a.S + QR - 1) / QR;
+
+  const int li = xcd_swizzle(blockIdx.x, a.Hkv * nslice * nqb);
+  const int g = li / (nslice * nqb);
+  const int rem = li % (nslice * nqb);
+  const int qb = nqb - 1 - rem / nslice;
+  const int slice = rem % nslice;
+  const int h = g * G + slice * HPW + wave % HPW;
+  const int row = qb * QR + (wave / HPW) * 32 + l32;
+  const int qt = (qb * QR) / kBlock;
+  const bool in = row < a.S;
+  const int qr = min(row, a.S - 1);
+
+  const T *qp = reinterpret_cast<const T *>(a.q) + h * a.q_sh + (int64_t)qr * a.q_ss;
+  const T *dop = reinterpret_cast<const T *>(a.dout) + h * a.do_sh + (int64_t)qr * a.do_ss;
+  const T *op = reinterpret_cast<const T *>(a.o) + h * a.o_sh + (int64_t)qr * a.o_ss;
+  const T *kp = reinterpret_cast<const T *>(a.k) + g * a.k_sh;
+  const T *vp = reinterpret_cast<const T *>(a.v) + g * a.v_sh;
+
+  bf16x8 qf[KS], df[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    qf[ks] = load8(qp + ks * 16 + hi * 8);
+    df[ks] = load8(dop + ks * 16 + hi * 8);
+  }
+  float del = half_row_dot<HD, T>(op, dop, hi);
+  del += xor32(del);
+  if (!in) del = 0.f;
+  if (in && hi == 0) a.delta[(int64_t)h * a.S + row] = del;
+  const float lse = in ? a.lse[(int64_t)h * a.S + row] : kNegInfD;
+  // a fully masked row has LSE -inf: it reaches no key (qlim = -1) and its P is 0
+  const float lse2 = lse == kNegInfD ? 0.f : lse * kLog2e;
+  const int qcode = in ? a.code[row] : kCodePad;
+  const int qlim = (qcode == kCodePad || lse == kNegInfD) ? -1 : row + a.P;
+
+  const int npart = a.kv_num[qt];
+  const int ntot = npart + a.fkv_num[qt];
+  const int32_t *pidx = a.kv_idx + (int64_t)qt * a.nKV;
+  const int32_t *fidx = a.fkv_idx + (int64_t)qt * a.nKV;
+  const int nstep = 2 * ntot;
+  TileList tiles{pidx, fidx, npart, ntot};
+  auto step_base = [&](int j) {
+    return tiles.at(j >> 1) * kBlock + (j & 1) * kStep;
+  };
+
+  const int krow_sw = swz<HD>(l32);
+  const TrLane tl = tr_lane<HD>(lane);
+
+  // bf16 operands go global -> LDS directly (no staging registers); fp32
+  // operands are converted through registers.
+  constexpr bool kDirect = sizeof(T) == 2;
+  TileStage<HD, kDirect ? 0 : kStep, T> stK, stV;
+  int creg = 0;
+  auto load_step = [&](int j, bf16_t *dK, bf16_t *dV) {
+    const int kb = step_base(j);
+    if constexpr (kDirect) {
+      tile_dma<HD, kStep>(dK, reinterpret_cast<const bf16_t *>(kp), a.k_ss, kb, a.L - 1);
+      tile_dma<HD, kStep>(dV, reinterpret_cast<const bf16_t *>(vp), a.v_ss, kb, a.L - 1);
+    } else {
+      stK.load(kp, a.k_ss, kb, a.L - 1);
+      stV.load(vp, a.v_ss, kb, a.L - 1);
+    }
+    if (tid < kStep) creg = key_code(a.code, kb + tid, a.P, a.L);
+  };
+  auto store_step = [&](bf16_t *dK, bf16_t *dV, int *dC) {
+    if constexpr (!kDirect) {
+      stK.store(dK);
+      stV.store(dV);
+    } else {
+      __builtin_amdgcn_s_waitcnt(0);   // this thread's direct loads have landed
+    }
+    if (tid < kStep) dC[tid] = creg;
+  };
+
+  f32x16 dqacc[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) dqacc[db] = zero16();
+
+  // one 64-key step reading buffer B while the next step loads into 1 - B
+  auto run_step = [&](auto bsel, int j) {
+    constexpr int B = decltype(bsel)::value;
+    bf16_t *tK = B ? sK1 : sK0;
+    bf16_t *tV = B ? sV1 : sV0;
+    const int *tC = B ? sC1 : sC0;
+    const int kbase = step_base(j);
+    const bool partial = (j >> 1) < npart;
+    if (j + 1 < nstep) load_step(j + 1, B ? sK0 : sK1, B ? sV0 : sV1);
+
+    if (kbase < a.L) {
+      // two 32-key halves of the 64-key tile (keeps the S / dP accumulators at 16 registers each)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        f32x16 sacc = zero16(), dpacc = zero16();
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          const int off = (kb * 32 + l32) * HD + (((2 * ks + hi) ^ krow_sw) << 3);
+          sacc = mfma32(lds_read8(tK + off), qf[ks], sacc);
+          dpacc = mfma32(lds_read8(tV + off), df[ks], dpacc);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int kl0 = kb * 32 + 8 * i + 4 * hi;
+          i32x4 kc = {kCodeX, kCodeX, kCodeX, kCodeX};
+          if (partial) kc = *reinterpret_cast<const i32x4 *>(&tC[kl0]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int r = 4 * i + e;
+            float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[r], a.scale_log2, -lse2));
+            if (partial) {
+              const bool ok = (kbase + kl0 + e <= qlim) & ((kc[e] == kCodeX) | (kc[e] == qcode));
+              p = ok ? p : 0.f;
+            } else {
+              p = qlim >= 0 ? p : 0.f;
+            }
+            dpacc[r] = p * (dpacc[r] - del);
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const bf16x8 dsb = pack8(dpacc[8 * u + 0], dpacc[8 * u + 1], dpacc[8 * u + 2], dpacc[8 * u + 3],
+                                   dpacc[8 * u + 4], dpacc[8 * u + 5], dpacc[8 * u + 6], dpacc[8 * u + 7]);
+#pragma unroll
+          for (int db = 0; db < DB; ++db)
+            dqacc[db] = mfma32(lds_tr_operand<HD>(tK, tl, kb * 32 + 16 * u, db), dsb, dqacc[db]);
+        }
+      }
+    }
+
+    if (j + 1 < nstep) store_step(B ? sK0 : sK1, B ? sV0 : sV1, B ? sC0 : sC1);
+    __syncthreads();
+  };
+
+  if (nstep > 0) {
+    load_step(0, sK0, sV0);
+    store_step(sK0, sV0, sC0);
+  }
+  __syncthreads();
+  for (int j = 0; j < nstep; j += 2) {
+    run_step(std::integral_constant<int, 0>{}, j);
+    if (j + 1 < nstep) run_step(std::integral_constant<int, 1>{}, j + 1);
+  }
+
+  if (in) {
+    T *row_out = reinterpret_cast<T *>(a.dq) + h * a.dq_sh + (int64_t)row * a.dq_ss;
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const f32x16 &c = dqacc[db];
+        store4(row_out + db * 32 + 8 * i + 4 * hi, c[4 * i] * a.scale, c[4 * i + 1] * a.scale,
+               c[4 * i + 2] * a.scale, c[4 * i + 3] * a.scale);
+      }
+  }
+}
+
+template <int HD, typename T>
+void dq_launch(const AttnArgs &a, hipStream_t st) {
+  const int G = a.Hq / a.Hkv;
+  const int HPW = heads_per_wg_dq(G);
+  const int QR = 32 * (4 / HPW);
+  const int nqb = (a.S + QR - 1) / QR;
+  hipLaunchKernelGGL((attn_bwd_dq_kernel<HD, T>), dim3(a.Hkv * (G / HPW) * nqb), dim3(256), 0, st, a);
+}
+
+template void dq_launch<128, bf16_t>(const AttnArgs &, hipStream_t);
+template void dq_launch<128, float>(const AttnArgs &, hipStream_t);
+template void dq_launch<64, bf16_t>(const AttnArgs &, hipStream_t);
+template void dq_launch<64, float>(const AttnArgs &, hipStream_t);
+
+}  // namespace mga

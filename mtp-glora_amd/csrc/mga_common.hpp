@@ -187,7 +187,7 @@ __device__ __forceinline__ bf16x8 lds_tr_operand(const bf16_t *tile, const TrLan
 template <int HD, int NR, typename T>
 struct TileStage {
   static constexpr int kGran = NR * HD / 8 / 256;
-  i32x4 reg[kGran];
+  i32x4 reg[kGran > 0 ? kGran : 1];
 
   __device__ __forceinline__ void load(const T *src, int64_t ss, int r0, int rmax) {
 #pragma unroll
@@ -206,6 +206,59 @@ struct TileStage {
       const int r = gi / (HD / 8), c = gi % (HD / 8);
       *reinterpret_cast<i32x4 *>(tile + tile_off<HD>(r, c)) = reg[i];
     }
+  }
+};
+
+}  // namespace mga
+
+namespace mga {
+
+// ---- direct global -> LDS staging of an NR x HD bf16 tile (4 waves) ---------
+// global_load_lds with 16 bytes per lane writes LDS at base + 16 * lane, so
+// each wave instruction fills one contiguous 1 KB block (1024 / (2 HD) rows);
+// lane picks the global granule that the swizzle places at its slot. Rows
+// beyond rmax repeat row rmax. Completion is tracked by vmcnt: wait for it
+// (and a barrier) before the tile is read.
+typedef __attribute__((address_space(3))) void lds_void;
+
+template <int HD, int NR>
+__device__ __forceinline__ void tile_dma(bf16_t *tile, const bf16_t *src, int64_t ss, int r0, int rmax) {
+  constexpr int kGranRow = HD / 8;                 // granules per row
+  constexpr int kRowsPerInst = 64 / kGranRow;      // rows per 1 KB block
+  constexpr int kInst = NR / kRowsPerInst / 4;     // blocks per wave
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int p = lane % kGranRow;
+#pragma unroll
+  for (int i = 0; i < kInst; ++i) {
+    const int blk = w * kInst + i;
+    const int r = blk * kRowsPerInst + lane / kGranRow;
+    const int c = p ^ swz<HD>(r);
+    const int row = min(r0 + r, rmax);
+    __builtin_amdgcn_global_load_lds(src + (int64_t)row * ss + c * 8, (lds_void *)(tile + blk * 512), 16, 0, 0);
+  }
+}
+
+}  // namespace mga
+
+namespace mga {
+
+// The block-mask tile list of one query tile (partial tiles, then full ones),
+// cached 64 entries at a time in a register (lane l holds entry base + l) and
+// read back with readlane, so a step's tile index costs no memory wait.
+struct TileList {
+  const int32_t *pidx, *fidx;
+  int npart, ntot;
+  int base = -64;
+  int val = 0;
+
+  __device__ __forceinline__ int at(int it) {   // it: wave-uniform, < ntot
+    const int cb = it & ~63;
+    if (cb != base) {
+      const int e = cb + (threadIdx.x & 63);
+      val = e < npart ? pidx[e] : (e < ntot ? fidx[e - npart] : 0);
+      base = cb;
+    }
+    return __builtin_amdgcn_readlane(val, it & 63);
   }
 };
 

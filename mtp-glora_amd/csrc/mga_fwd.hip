@@ -83,10 +83,9 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
   const int32_t *pidx = a.kv_idx + (int64_t)qt * a.nKV;
   const int32_t *fidx = a.fkv_idx + (int64_t)qt * a.nKV;
   const int nstep = 2 * ntot;
+  TileList tiles{pidx, fidx, npart, ntot};
   auto step_base = [&](int j) {
-    const int it = j >> 1;
-    const int kt = it < npart ? pidx[it] : fidx[it - npart];
-    return kt * kBlock + (j & 1) * kStepKeys;
+    return tiles.at(j >> 1) * kBlock + (j & 1) * kStepKeys;
   };
 
   // per-lane LDS offsets: K rows (A operand of QK^T) and the V^T transpose reads
