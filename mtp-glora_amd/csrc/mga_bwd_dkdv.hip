@@ -35,7 +35,8 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(AttnArgs a, int k
   constexpr int TILE = kQStep * HD;
   __shared__ __attribute__((aligned(16))) bf16_t sQ0[TILE], sQ1[TILE];
   __shared__ __attribute__((aligned(16))) bf16_t sD0[TILE], sD1[TILE];
-  // per query row of the step: lse * log2(e), delta, causal bound (-1: sees nothing), code
+  // per query row of the step: lse * log2(e), delta, causal bound (-1: sees nothing),
+  // ordered-compare value (query_v)
   __shared__ __attribute__((aligned(16))) float sL0[kQStep], sL1[kQStep];
   __shared__ __attribute__((aligned(16))) float sE0[kQStep], sE1[kQStep];
   __shared__ __attribute__((aligned(16))) int sM0[kQStep], sM1[kQStep];
@@ -56,8 +57,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(AttnArgs a, int k
 
   const int key = kt * kBlock + wave * 32 + l32;
   const int kr = min(key, a.L - 1);
-  const int kcode = key_code(a.code, key, a.P, a.L);
-  const bool kx = kcode == kCodeX;
+  const int kw = key_w(a.code, key, a.P, a.L);
 
   bf16x8 kf[KS], vf[KS];
   {
@@ -83,8 +83,10 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(AttnArgs a, int k
 
   constexpr bool kDirect = sizeof(T) == 2;
   TileStage<HD, kDirect ? 0 : kQStep, T> stQ, stD;
+  // per query row of the next step: raw lse, delta and code, converted at
+  // store time (converting here would wait for the tile loads in flight)
   float rl = 0.f, re = 0.f;
-  int rm = -1, rc = kCodePad;
+  int rc = kCodePad, rq = 0;
   auto load_step = [&](int j, bf16_t *dQ, bf16_t *dD) {
     const int q0 = step_base(j);
     if constexpr (kDirect) {
@@ -95,14 +97,12 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(AttnArgs a, int k
       stD.load(dop, a.do_ss, q0, a.S - 1);
     }
     if (tid < kQStep) {
-      const int q = q0 + tid;
-      const bool in = q < a.S;
-      const float lse = in ? a.lse[(int64_t)h * a.S + q] : kNegInfK;
-      const int code = in ? a.code[q] : kCodePad;
-      rl = lse == kNegInfK ? 0.f : lse * kLog2e;
-      re = in ? a.delta[(int64_t)h * a.S + q] : 0.f;
-      rm = (code == kCodePad || lse == kNegInfK) ? -1 : q + a.P;
-      rc = code;
+      rq = q0 + tid;
+      if (rq < a.S) {
+        rl = a.lse[(int64_t)h * a.S + rq];
+        re = a.delta[(int64_t)h * a.S + rq];
+        rc = a.code[rq];
+      }
     }
   };
   auto store_step = [&](bf16_t *dQ, bf16_t *dD, float *dL, float *dE, int *dM, int *dC) {
@@ -113,10 +113,13 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(AttnArgs a, int k
       __builtin_amdgcn_s_waitcnt(0);
     }
     if (tid < kQStep) {
-      dL[tid] = rl;
-      dE[tid] = re;
-      dM[tid] = rm;
-      dC[tid] = rc;
+      const bool in = rq < a.S;
+      const int code = in ? rc : kCodePad;
+      const float lse = in ? rl : kNegInfK;
+      dL[tid] = lse == kNegInfK ? 0.f : lse * kLog2e;
+      dE[tid] = in ? re : 0.f;
+      dM[tid] = (code == kCodePad || lse == kNegInfK) ? -1 : rq + a.P;   // causal bound, -1: sees nothing
+      dC[tid] = query_v(code);
     }
   };
 
@@ -151,17 +154,17 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(AttnArgs a, int k
           const int ql0 = qb * 32 + 8 * i + 4 * hi;
           const f32x4 l4 = *reinterpret_cast<const f32x4 *>(&tL[ql0]);
           const f32x4 e4 = *reinterpret_cast<const f32x4 *>(&tE[ql0]);
-          i32x4 m4 = {-1, -1, -1, -1}, c4 = {kCodePad, kCodePad, kCodePad, kCodePad};
+          i32x4 m4 = {-1, -1, -1, -1}, v4 = {kWX, kWX, kWX, kWX};
           if (partial) {
             m4 = *reinterpret_cast<const i32x4 *>(&tM[ql0]);
-            c4 = *reinterpret_cast<const i32x4 *>(&tC[ql0]);
+            v4 = *reinterpret_cast<const i32x4 *>(&tC[ql0]);
           }
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const int r = 4 * i + e;
             float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[r], a.scale_log2, -l4[e]));
             if (partial) {
-              const bool ok = (key <= m4[e]) & (kx | (kcode == c4[e]));
+              const bool ok = (key <= m4[e]) & (kw >= v4[e]);
               p = ok ? p : 0.f;
             }
             sacc[r] = p;

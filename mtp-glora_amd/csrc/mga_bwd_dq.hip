@@ -2,7 +2,9 @@
 //
 // Same work decomposition as the forward (mga_fwd.hip): a workgroup of 4 waves
 // holds 4 (query head, 32-row block) pairs of one kv head, so each staged K/V
-// tile feeds four heads. Per 64-key step each wave computes
+// tile feeds four heads. Q stays in registers; each lane parks its dO row in
+// LDS (read back only by itself: register relief that costs no memory wait).
+// Per 32-key step each wave computes
 //   S^T  = K Q^T,  dP^T = V dO^T                    (A operands: K, V rows)
 //   P    = exp2(S^T * scale_log2 - lse_log2)         (0 where masked)
 //   dS^T = P (dP^T - delta)
@@ -21,7 +23,7 @@ namespace mga {
 namespace {
 
 constexpr float kNegInfD = -__builtin_huge_valf();
-constexpr int kStep = 64;
+constexpr int kStep = 32;
 
 __host__ __device__ __forceinline__ int heads_per_wg_dq(int G) { return (G % 4 == 0) ? 4 : (G % 2 == 0 ? 2 : 1); }
 
@@ -58,7 +60,8 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnArgs a) {
   // reads of the other, so it does not wait for them before computing
   __shared__ __attribute__((aligned(16))) bf16_t sK0[TILE], sK1[TILE];
   __shared__ __attribute__((aligned(16))) bf16_t sV0[TILE], sV1[TILE];
-  __shared__ __attribute__((aligned(16))) int sC0[kStep], sC1[kStep];
+  __shared__ __attribute__((aligned(16))) int sW0[kStep], sW1[kStep];
+  __shared__ __attribute__((aligned(16))) bf16_t sDO[4][32 * HD];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, hi = lane >> 5;
@@ -85,11 +88,15 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnArgs a) {
   const T *kp = reinterpret_cast<const T *>(a.k) + g * a.k_sh;
   const T *vp = reinterpret_cast<const T *>(a.v) + g * a.v_sh;
 
-  bf16x8 qf[KS], df[KS];
+  // Q fragments in registers; this lane's dO half-row granules to its own LDS row
+  const int krow_sw = swz<HD>(l32);
+  bf16_t *myDO = sDO[wave];
+  bf16x8 qf[KS];
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
     qf[ks] = load8(qp + ks * 16 + hi * 8);
-    df[ks] = load8(dop + ks * 16 + hi * 8);
+    *reinterpret_cast<i32x4 *>(myDO + l32 * HD + (((2 * ks + hi) ^ krow_sw) << 3)) =
+        __builtin_bit_cast(i32x4, load8(dop + ks * 16 + hi * 8));
   }
   float del = half_row_dot<HD, T>(op, dop, hi);
   del += xor32(del);
@@ -99,108 +106,108 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnArgs a) {
   // a fully masked row has LSE -inf: it reaches no key (qlim = -1) and its P is 0
   const float lse2 = lse == kNegInfD ? 0.f : lse * kLog2e;
   const int qcode = in ? a.code[row] : kCodePad;
+  const int qv = query_v(qcode);
   const int qlim = (qcode == kCodePad || lse == kNegInfD) ? -1 : row + a.P;
 
   const int npart = a.kv_num[qt];
   const int ntot = npart + a.fkv_num[qt];
-  const int32_t *pidx = a.kv_idx + (int64_t)qt * a.nKV;
-  const int32_t *fidx = a.fkv_idx + (int64_t)qt * a.nKV;
-  const int nstep = 2 * ntot;
-  TileList tiles{pidx, fidx, npart, ntot};
-  auto step_base = [&](int j) {
-    return tiles.at(j >> 1) * kBlock + (j & 1) * kStep;
-  };
+  TileList tiles{a.kv_idx + (int64_t)qt * a.nKV, a.fkv_idx + (int64_t)qt * a.nKV, npart, ntot};
+  constexpr int kSub = kBlock / kStep;      // steps per 128-key tile
+  const int nstep = kSub * ntot;
+  auto step_base = [&](int j) { return tiles.at(j / kSub) * kBlock + (j % kSub) * kStep; };
 
-  const int krow_sw = swz<HD>(l32);
   const TrLane tl = tr_lane<HD>(lane);
 
   // bf16 operands go global -> LDS directly (no staging registers); fp32
   // operands are converted through registers.
   constexpr bool kDirect = sizeof(T) == 2;
   TileStage<HD, kDirect ? 0 : kStep, T> stK, stV;
-  int creg = 0;
+  KeyCode knext;
   auto load_step = [&](int j, bf16_t *dK, bf16_t *dV) {
     const int kb = step_base(j);
     if constexpr (kDirect) {
-      tile_dma<HD, kStep>(dK, reinterpret_cast<const bf16_t *>(kp), a.k_ss, kb, a.L - 1);
-      tile_dma<HD, kStep>(dV, reinterpret_cast<const bf16_t *>(vp), a.v_ss, kb, a.L - 1);
+      if (kb < a.L) {   // a step past the keys is never computed: nothing to load
+        tile_dma<HD, kStep>(dK, reinterpret_cast<const bf16_t *>(kp), a.k_ss, kb, a.L - 1);
+        tile_dma<HD, kStep>(dV, reinterpret_cast<const bf16_t *>(vp), a.v_ss, kb, a.L - 1);
+      }
     } else {
       stK.load(kp, a.k_ss, kb, a.L - 1);
       stV.load(vp, a.v_ss, kb, a.L - 1);
     }
-    if (tid < kStep) creg = key_code(a.code, kb + tid, a.P, a.L);
+    if (tid < kStep) knext.load(a.code, kb + tid, a.P, a.L);   // converted at store time
   };
-  auto store_step = [&](bf16_t *dK, bf16_t *dV, int *dC) {
+  auto store_step = [&](bf16_t *dK, bf16_t *dV, int *dW) {
     if constexpr (!kDirect) {
       stK.store(dK);
       stV.store(dV);
     } else {
       __builtin_amdgcn_s_waitcnt(0);   // this thread's direct loads have landed
     }
-    if (tid < kStep) dC[tid] = creg;
+    if (tid < kStep) dW[tid] = knext.w();
   };
 
   f32x16 dqacc[DB];
 #pragma unroll
   for (int db = 0; db < DB; ++db) dqacc[db] = zero16();
 
-  // one 64-key step reading buffer B while the next step loads into 1 - B
+  // one 32-key step reading buffer B while the next step loads into 1 - B
   auto run_step = [&](auto bsel, int j) {
     constexpr int B = decltype(bsel)::value;
-    bf16_t *tK = B ? sK1 : sK0;
-    bf16_t *tV = B ? sV1 : sV0;
-    const int *tC = B ? sC1 : sC0;
+    const bf16_t *tK = B ? sK1 : sK0;
+    const bf16_t *tV = B ? sV1 : sV0;
+    const int *tW = B ? sW1 : sW0;
     const int kbase = step_base(j);
-    const bool partial = (j >> 1) < npart;
+    const bool partial = (j / kSub) < npart;
     if (j + 1 < nstep) load_step(j + 1, B ? sK0 : sK1, B ? sV0 : sV1);
 
     if (kbase < a.L) {
-      // two 32-key halves of the 64-key tile (keeps the S / dP accumulators at 16 registers each)
+      // S^T = K Q^T and dP^T - delta = V dO^T - delta (the accumulator starts at
+      // -delta); register r is key kbase + 8 (r / 4) + 4 hi + r % 4
+      f32x16 sacc = zero16(), dpacc;
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        f32x16 sacc = zero16(), dpacc = zero16();
+      for (int r = 0; r < 16; ++r) dpacc[r] = -del;
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-          const int off = (kb * 32 + l32) * HD + (((2 * ks + hi) ^ krow_sw) << 3);
-          sacc = mfma32(lds_read8(tK + off), qf[ks], sacc);
-          dpacc = mfma32(lds_read8(tV + off), df[ks], dpacc);
-        }
+      for (int ks = 0; ks < KS; ++ks) {
+        const int off = l32 * HD + (((2 * ks + hi) ^ krow_sw) << 3);
+        sacc = mfma32(lds_read8(tK + off), qf[ks], sacc);
+        dpacc = mfma32(lds_read8(tV + off), lds_read8(myDO + off), dpacc);
+      }
+      const int lim = qlim - kbase - 4 * hi;   // causal: key offset (without 4 hi) <= lim
+      const bool diag = partial && __builtin_amdgcn_ballot_w64(lim < kStep - 1) != 0;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int kl0 = kb * 32 + 8 * i + 4 * hi;
-          i32x4 kc = {kCodeX, kCodeX, kCodeX, kCodeX};
-          if (partial) kc = *reinterpret_cast<const i32x4 *>(&tC[kl0]);
+      for (int i = 0; i < 4; ++i) {
+        i32x4 w4 = {kWX, kWX, kWX, kWX};
+        if (partial) w4 = *reinterpret_cast<const i32x4 *>(&tW[8 * i + 4 * hi]);
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int r = 4 * i + e;
-            float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[r], a.scale_log2, -lse2));
-            if (partial) {
-              const bool ok = (kbase + kl0 + e <= qlim) & ((kc[e] == kCodeX) | (kc[e] == qcode));
-              p = ok ? p : 0.f;
-            } else {
-              p = qlim >= 0 ? p : 0.f;
-            }
-            dpacc[r] = p * (dpacc[r] - del);
+        for (int e = 0; e < 4; ++e) {
+          const int r = 4 * i + e;
+          float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[r], a.scale_log2, -lse2));
+          if (partial) {
+            bool ok = w4[e] >= qv;
+            if (diag) ok = ok & (8 * i + e <= lim);
+            p = ok ? p : 0.f;
           }
+          dpacc[r] = p * dpacc[r];
         }
+      }
+      // dQ^T += K^T dS^T
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const bf16x8 dsb = pack8(dpacc[8 * u + 0], dpacc[8 * u + 1], dpacc[8 * u + 2], dpacc[8 * u + 3],
-                                   dpacc[8 * u + 4], dpacc[8 * u + 5], dpacc[8 * u + 6], dpacc[8 * u + 7]);
+      for (int u = 0; u < 2; ++u) {
+        const bf16x8 dsb = pack8(dpacc[8 * u + 0], dpacc[8 * u + 1], dpacc[8 * u + 2], dpacc[8 * u + 3],
+                                 dpacc[8 * u + 4], dpacc[8 * u + 5], dpacc[8 * u + 6], dpacc[8 * u + 7]);
 #pragma unroll
-          for (int db = 0; db < DB; ++db)
-            dqacc[db] = mfma32(lds_tr_operand<HD>(tK, tl, kb * 32 + 16 * u, db), dsb, dqacc[db]);
-        }
+        for (int db = 0; db < DB; ++db)
+          dqacc[db] = mfma32(lds_tr_operand<HD>(tK, tl, 16 * u, db), dsb, dqacc[db]);
       }
     }
 
-    if (j + 1 < nstep) store_step(B ? sK0 : sK1, B ? sV0 : sV1, B ? sC0 : sC1);
+    if (j + 1 < nstep) store_step(B ? sK0 : sK1, B ? sV0 : sV1, B ? sW0 : sW1);
     __syncthreads();
   };
 
   if (nstep > 0) {
     load_step(0, sK0, sV0);
-    store_step(sK0, sV0, sC0);
+    store_step(sK0, sV0, sW0);
   }
   __syncthreads();
   for (int j = 0; j < nstep; j += 2) {

@@ -39,6 +39,9 @@ int check_operand(const char *name, const void *p, int64_t sh, int64_t ss, int e
   if (!aligned16(p)) return fail(MGA_ERR_INVALID, "%s: base pointer not 16-byte aligned", name);
   if (sh < 0 || ss <= 0) return fail(MGA_ERR_INVALID, "%s: invalid strides (%lld, %lld)", name,
                                       (long long)sh, (long long)ss);
+  // tile loads address up to 128 rows with 32-bit per-lane offsets
+  if (ss >= (int64_t(1) << 23))
+    return fail(MGA_ERR_INVALID, "%s: row stride %lld elements is too large (limit 2^23)", name, (long long)ss);
   if (((sh * eb) & 15) || ((ss * eb) & 15))
     return fail(MGA_ERR_INVALID, "%s: strides (%lld, %lld) elements are not multiples of 16 bytes",
                 name, (long long)sh, (long long)ss);

@@ -263,3 +263,85 @@ struct TileList {
 };
 
 }  // namespace mga
+
+namespace mga {
+
+constexpr int kWX = 0x7fffffff;      // ordered-compare value of a regular key / query
+constexpr int kWPad = -0x7fffffff;   // ordered-compare value of a pad key
+
+// Ordered-compare form of the MTP predicate: allowed(q, k) = (k <= qlim(q)) &
+// (key_w(k) >= query_v(q)). A mask key at or before the query carries a code
+// (num_prefix_x) no larger than the query's, equal exactly within the query's
+// own block, so one compare replaces "key is regular or in the same block".
+__device__ __forceinline__ int key_w(const int32_t *code, int key, int P, int L) {
+  if (key < P) return kWX;
+  if (key >= L) return kWPad;
+  const int c = code[key - P];
+  return c == kCodeX ? kWX : (c == kCodePad ? kWPad : c);
+}
+
+__device__ __forceinline__ int query_v(int qcode) { return qcode == kCodeX ? kWX : qcode; }
+
+// Per-lane element offsets of the direct loads of an NR x HD tile whose rows
+// are r0 .. r0 + NR - 1 of a source with row stride ss (see tile_dma). With
+// these the load address is a wave-uniform row base plus a lane constant.
+template <int HD, int NR>
+struct DmaLane {
+  static constexpr int kGranRow = HD / 8;
+  static constexpr int kRowsPerInst = 64 / kGranRow;
+  static constexpr int kInst = NR / kRowsPerInst / 4;
+  uint32_t off[kInst];   // bytes
+  __device__ __forceinline__ void init(int64_t ss) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int p = lane % kGranRow;
+#pragma unroll
+    for (int i = 0; i < kInst; ++i) {
+      const int r = (w * kInst + i) * kRowsPerInst + lane / kGranRow;
+      off[i] = (uint32_t)(r * ss * 2) + (uint32_t)((p ^ swz<HD>(r)) << 4);
+    }
+  }
+  // only rows 0 .. nvalid - 1 of the tile exist, 1 <= nvalid < NR (callers
+  // issue nothing for a tile with no rows): later rows repeat the last one
+  __device__ __forceinline__ void issue_clamped(bf16_t *tile, const bf16_t *rowbase, int64_t ss,
+                                                int nvalid) const {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int p = lane % kGranRow;
+    const char *base = reinterpret_cast<const char *>(rowbase);
+#pragma unroll
+    for (int i = 0; i < kInst; ++i) {
+      const int r = (w * kInst + i) * kRowsPerInst + lane / kGranRow;
+      const uint32_t o = (uint32_t)(min(r, nvalid - 1) * (int)ss * 2) + (uint32_t)((p ^ swz<HD>(r)) << 4);
+      __builtin_amdgcn_global_load_lds(base + o, (lds_void *)(tile + (w * kInst + i) * 512), 16, 0, 0);
+    }
+  }
+  // rows r0 .. r0 + NR - 1 all exist in the source; rowbase is wave-uniform
+  __device__ __forceinline__ void issue(bf16_t *tile, const bf16_t *rowbase) const {
+    const int w = threadIdx.x >> 6;
+    const char *base = reinterpret_cast<const char *>(rowbase);
+#pragma unroll
+    for (int i = 0; i < kInst; ++i)
+      __builtin_amdgcn_global_load_lds(base + off[i], (lds_void *)(tile + (w * kInst + i) * 512), 16, 0, 0);
+  }
+};
+
+}  // namespace mga
+
+namespace mga {
+
+// A key's code fetched one step ahead: load() only issues the read (so it does
+// not wait on the tile loads in flight), w() converts at store time.
+struct KeyCode {
+  int raw = 0;
+  int kind = 0;   // 0: chunk key (raw = its code), 1: cached prefix key, 2: past the end
+  __device__ __forceinline__ void load(const int32_t *code, int key, int P, int L) {
+    kind = key < P ? 1 : (key >= L ? 2 : 0);
+    if (kind == 0) raw = code[key - P];
+  }
+  __device__ __forceinline__ int w() const {
+    if (kind == 1) return kWX;
+    if (kind == 2) return kWPad;
+    return raw == kCodeX ? kWX : (raw == kCodePad ? kWPad : raw);
+  }
+};
+
+}  // namespace mga

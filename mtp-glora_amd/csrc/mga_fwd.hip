@@ -9,14 +9,18 @@
 // (plus one exchange with the lane 32 away) and accumulates O^T += V^T P^T,
 // feeding the probabilities from the accumulator registers straight into the
 // B operand. V^T comes from the row-major V tile through the LDS transpose
-// read. K/V tiles are prefetched into registers one step ahead and written
-// to a second LDS buffer, so one barrier per step suffices.
+// read. bf16 K/V tiles are loaded one step ahead straight into the other of
+// two named LDS buffers, so one barrier per step suffices.
 //
 // Rescaling of O is lazy: the running max only moves when a new score exceeds
 // it by more than 2^8 (log2 domain), which keeps every probability below 256
 // and leaves the result exact up to rounding (the final normalisation uses the
-// same max). Semantics: [torch]_higher_order_ops/flex_attention.py:202-267
-// (masked scores are -inf; a fully masked row has output 0 and LSE -inf).
+// same max). Masking on partial tiles is one ordered compare per score (see
+// key_w) plus the causal bound on the steps that cross the diagonal.
+// Semantics: [torch]_higher_order_ops/flex_attention.py:202-267 (masked
+// scores -inf; a fully masked row has output 0 and LSE -inf).
+#include <type_traits>
+
 #include "mga_common.hpp"
 #include "mga_internal.hpp"
 
@@ -40,9 +44,9 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
   constexpr int KS = HD / 16;          // k-steps of QK^T over head_dim
   constexpr int DB = HD / 32;          // 32-dim blocks of O^T
   constexpr int TILE = kStepKeys * HD; // elements of one K or V step tile
-  __shared__ __attribute__((aligned(16))) bf16_t sK[2][TILE];
-  __shared__ __attribute__((aligned(16))) bf16_t sV[2][TILE];
-  __shared__ __attribute__((aligned(16))) int sC[2][kStepKeys];
+  __shared__ __attribute__((aligned(16))) bf16_t sK0[TILE], sK1[TILE];
+  __shared__ __attribute__((aligned(16))) bf16_t sV0[TILE], sV1[TILE];
+  __shared__ __attribute__((aligned(16))) int sW0[kStepKeys], sW1[kStepKeys];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, hi = lane >> 5;
@@ -75,35 +79,55 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
     for (int ks = 0; ks < KS; ++ks) qf[ks] = load8(qp + (int64_t)qr * a.q_ss + ks * 16 + hi * 8);
   }
   const int qcode = row < a.S ? a.code[row] : kCodePad;
+  const int qv = query_v(qcode);
   // a pad query (or a row past S) sees no key: fold that into the causal bound
   const int qlim = (qcode == kCodePad) ? -1 : row + a.P;
 
   const int npart = a.kv_num[qt];
   const int ntot = npart + a.fkv_num[qt];
-  const int32_t *pidx = a.kv_idx + (int64_t)qt * a.nKV;
-  const int32_t *fidx = a.fkv_idx + (int64_t)qt * a.nKV;
+  TileList tiles{a.kv_idx + (int64_t)qt * a.nKV, a.fkv_idx + (int64_t)qt * a.nKV, npart, ntot};
   const int nstep = 2 * ntot;
-  TileList tiles{pidx, fidx, npart, ntot};
-  auto step_base = [&](int j) {
-    return tiles.at(j >> 1) * kBlock + (j & 1) * kStepKeys;
-  };
+  auto step_base = [&](int j) { return tiles.at(j >> 1) * kBlock + (j & 1) * kStepKeys; };
 
   // per-lane LDS offsets: K rows (A operand of QK^T) and the V^T transpose reads
   const int krow_sw = swz<HD>(l32);
   const TrLane tl = tr_lane<HD>(lane);
 
-  TileStage<HD, kStepKeys, T> stK, stV;
-  int creg = 0;
-  auto load_step = [&](int j) {
+  constexpr bool kDirect = sizeof(T) == 2;
+  DmaLane<HD, kStepKeys> dmaK, dmaV;
+  if constexpr (kDirect) {
+    dmaK.init(a.k_ss);
+    dmaV.init(a.v_ss);
+  }
+  TileStage<HD, kDirect ? 0 : kStepKeys, T> stK, stV;
+  KeyCode wkey;
+  auto load_step = [&](int j, bf16_t *dK, bf16_t *dV) {
     const int kb = step_base(j);
-    stK.load(kp, a.k_ss, kb, a.L - 1);
-    stV.load(vp, a.v_ss, kb, a.L - 1);
-    if (tid < kStepKeys) creg = key_code(a.code, kb + tid, a.P, a.L);
+    if constexpr (kDirect) {
+      if (kb >= a.L) {
+        // second half of the last tile, past the keys: never computed, nothing to load
+      } else if (kb + kStepKeys <= a.L) {
+        dmaK.issue(dK, reinterpret_cast<const bf16_t *>(kp) + (int64_t)kb * a.k_ss);
+        dmaV.issue(dV, reinterpret_cast<const bf16_t *>(vp) + (int64_t)kb * a.v_ss);
+      } else {
+        dmaK.issue_clamped(dK, reinterpret_cast<const bf16_t *>(kp) + (int64_t)kb * a.k_ss, a.k_ss, a.L - kb);
+        dmaV.issue_clamped(dV, reinterpret_cast<const bf16_t *>(vp) + (int64_t)kb * a.v_ss, a.v_ss, a.L - kb);
+      }
+    } else {
+      stK.load(kp, a.k_ss, kb, a.L - 1);
+      stV.load(vp, a.v_ss, kb, a.L - 1);
+    }
+    // raw code only: converting it here would wait for the tile loads too
+    if (tid < kStepKeys) wkey.load(a.code, kb + tid, a.P, a.L);
   };
-  auto store_step = [&](int buf) {
-    stK.store(sK[buf]);
-    stV.store(sV[buf]);
-    if (tid < kStepKeys) sC[buf][tid] = creg;
+  auto store_step = [&](bf16_t *dK, bf16_t *dV, int *dW) {
+    if constexpr (kDirect) {
+      __builtin_amdgcn_s_waitcnt(0);   // this thread's direct loads have landed
+    } else {
+      stK.store(dK);
+      stV.store(dV);
+    }
+    if (tid < kStepKeys) dW[tid] = wkey.w();
   };
 
   float m_run = kNegInfF, m_use = 0.f, l_run = 0.f;
@@ -111,71 +135,62 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
 #pragma unroll
   for (int db = 0; db < DB; ++db) oacc[db] = zero16();
 
-  if (nstep > 0) {
-    load_step(0);
-    store_step(0);
-  }
-  __syncthreads();
-
-  for (int j = 0; j < nstep; ++j) {
-    const int buf = j & 1;
+  auto run_step = [&](auto bsel, int j) {
+    constexpr int B = decltype(bsel)::value;
+    const bf16_t *tK = B ? sK1 : sK0;
+    const bf16_t *tV = B ? sV1 : sV0;
+    const int *tW = B ? sW1 : sW0;
     const int kbase = step_base(j);
     const bool partial = (j >> 1) < npart;
-    if (j + 1 < nstep) load_step(j + 1);
+    if (j + 1 < nstep) load_step(j + 1, B ? sK0 : sK1, B ? sV0 : sV1);
 
     if (kbase < a.L) {
-      const bf16_t *tK = sK[buf];
-      const bf16_t *tV = sV[buf];
-      // ---- S^T = K Q^T for 64 keys x 32 queries -----------------------------
+      // S^T = K Q^T for 64 keys x 32 queries; register r of sacc[kb] is key
+      // kb * 32 + 8 (r / 4) + 4 hi + r % 4 of the step
       f32x16 sacc[2] = {zero16(), zero16()};
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
+      for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
-          const int r = kb * 32 + l32;
-          const bf16x8 af = lds_read8(tK + r * HD + (((2 * ks + hi) ^ krow_sw) << 3));
+          const bf16x8 af = lds_read8(tK + (kb * 32 + l32) * HD + (((2 * ks + hi) ^ krow_sw) << 3));
           sacc[kb] = mfma32(af, qf[ks], sacc[kb]);
         }
-      }
-      // ---- mask, running max -------------------------------------------------
-      float mx = kNegInfF;
       if (partial) {
+        const int lim = qlim - kbase - 4 * hi;   // key offset (without 4 hi) must be <= lim
+        const bool diag = __builtin_amdgcn_ballot_w64(lim < kStepKeys - 1) != 0;
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const int kl0 = kb * 32 + 8 * i + 4 * hi;
-            const i32x4 kc = *reinterpret_cast<const i32x4 *>(&sC[buf][kl0]);
+            const i32x4 w4 = *reinterpret_cast<const i32x4 *>(&tW[kb * 32 + 8 * i + 4 * hi]);
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-              const bool ok = (kbase + kl0 + e <= qlim) & ((kc[e] == kCodeX) | (kc[e] == qcode));
-              const float s = ok ? sacc[kb][4 * i + e] : kNegInfF;
-              sacc[kb][4 * i + e] = s;
-              mx = fmaxf(mx, s);
+              bool ok = w4[e] >= qv;
+              if (diag) ok = ok & (kb * 32 + 8 * i + e <= lim);
+              sacc[kb][4 * i + e] = ok ? sacc[kb][4 * i + e] : kNegInfF;
             }
           }
-      } else {
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kb][r]);
       }
+      // running max with lazy rescale: m moves only when a score exceeds it by 2^8
+      float mx = kNegInfF;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kb][r]);
       mx = fmaxf(mx, xor32(mx)) * a.scale_log2;
-      const bool need = mx > m_run + kLazyMax;
-      if (__builtin_amdgcn_ballot_w64(need)) {
+      if (__builtin_amdgcn_ballot_w64(mx > m_run + kLazyMax)) {
         const float m_new = fmaxf(m_run, mx);
-        const float alpha = exp2f_(m_run - m_new);     // 0 when m_run = -inf
         if (m_new != m_run) {
+          const float alpha = exp2f_(m_run - m_new);   // 0 when m_run = -inf
           l_run *= alpha;
 #pragma unroll
           for (int db = 0; db < DB; ++db)
 #pragma unroll
             for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
+          m_run = m_new;
         }
-        m_run = m_new;
         m_use = m_run == kNegInfF ? 0.f : m_run;
       }
-      // ---- P = exp2(s * scale_log2 - m) ----------------------------------------
       float ps = 0.f;
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
@@ -186,7 +201,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
           ps += p;
         }
       l_run += ps;
-      // ---- O^T += V^T P^T ------------------------------------------------------
+      // O^T += V^T P^T
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -195,15 +210,23 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
           const bf16x8 pb = pack8(s[8 * u + 0], s[8 * u + 1], s[8 * u + 2], s[8 * u + 3],
                                   s[8 * u + 4], s[8 * u + 5], s[8 * u + 6], s[8 * u + 7]);
 #pragma unroll
-          for (int db = 0; db < DB; ++db) {
-            const bf16x8 af = lds_tr_operand<HD>(tV, tl, kb * 32 + 16 * u, db);
-            oacc[db] = mfma32(af, pb, oacc[db]);
-          }
+          for (int db = 0; db < DB; ++db)
+            oacc[db] = mfma32(lds_tr_operand<HD>(tV, tl, kb * 32 + 16 * u, db), pb, oacc[db]);
         }
     }
 
-    if (j + 1 < nstep) store_step(buf ^ 1);
+    if (j + 1 < nstep) store_step(B ? sK0 : sK1, B ? sV0 : sV1, B ? sW0 : sW1);
     __syncthreads();
+  };
+
+  if (nstep > 0) {
+    load_step(0, sK0, sV0);
+    store_step(sK0, sV0, sW0);
+  }
+  __syncthreads();
+  for (int j = 0; j < nstep; j += 2) {
+    run_step(std::integral_constant<int, 0>{}, j);
+    if (j + 1 < nstep) run_step(std::integral_constant<int, 1>{}, j + 1);
   }
 
   // ---- epilogue: normalise, write O [S, Hq, D] and the natural-log LSE -------

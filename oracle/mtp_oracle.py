@@ -16,7 +16,9 @@ installed torch / transformers trees):
 * ``mtp_mask_dense``                     - the MTP ``mask_mod`` predicate of
   ``collator.py:311-355`` over ``[S, P+S]``.
 * ``mtp_codes``                          - one int32 code per chunk token
-  (pad -1, x -2, m -> num_prefix_x) that encodes the same predicate.
+  (pad -1, x -2, m -> num_prefix_x) that encodes the same predicate;
+  ``mask_from_codes`` / ``mask_from_order`` rebuild it in the two forms the
+  GPU kernels evaluate.
 * ``block_mask_from_dense``              - ``create_block_mask``'s tile
   classification and ordering, ``[torch]nn/attention/flex_attention.py``
   ``:399-442`` (``_ordered_to_dense``/``_dense_to_ordered``/
@@ -239,6 +241,27 @@ def mask_from_codes(code: np.ndarray, P: int) -> np.ndarray:
     qc = code[:, None]
     kc = kcode[None, :]
     return (qi >= kj) & (qc != CODE_PAD) & ((kc == CODE_X) | (kc == qc))
+
+
+def mask_from_order(code: np.ndarray, P: int) -> np.ndarray:
+    """The predicate as one causal bound and one ordered compare, the form the
+    GPU kernels evaluate: with w(key) = +inf for a regular key, -inf for a
+    pad key, else its num_prefix_x code, and v(query) = +inf for a regular
+    query, else its code,
+
+        allowed(i, j) = (j <= qlim(i)) & (w(j) >= v(i)),  qlim = -1 for a pad query.
+
+    Equal to ``mask_from_codes`` because num_prefix_x never decreases along the
+    sequence, so a mask key at or before the query carries a code <= the
+    query's, with equality exactly for keys of the query's own block."""
+    big = np.int64(2 ** 31 - 1)
+    S = len(code)
+    c = code.astype(np.int64)
+    kcode = np.concatenate([np.full(P, CODE_X, np.int64), c])
+    w = np.where(kcode == CODE_X, big, np.where(kcode == CODE_PAD, -big, kcode))
+    v = np.where(c == CODE_X, big, c)
+    qlim = np.where(c == CODE_PAD, -1, np.arange(S) + P)
+    return (np.arange(P + S)[None, :] <= qlim[:, None]) & (w[None, :] >= v[:, None])
 
 
 # ----------------------------------------------------------------------------

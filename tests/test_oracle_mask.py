@@ -187,3 +187,19 @@ def test_cache_append_equals_reference_cat():
                                        torch.tensor(reg)[None])
     assert np.array_equal(mo.cache_append(prefix, cur, reg), out[0].numpy())
     assert full.shape[2] == 16
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_ordered_compare_form_equals_predicate(seed):
+    """The single ordered compare the GPU kernels evaluate equals the
+    reference predicate, on real layouts and on arbitrary gate vectors (pads
+    and gate-0 tokens anywhere, which the predicate still defines)."""
+    rng = np.random.default_rng(100 + seed)
+    for _ in range(400):
+        n_reg = int(rng.integers(1, 50))
+        D = int(rng.integers(1, 9))
+        seq = random_seq(rng, n_reg, int(rng.integers(0, n_reg + 1)), D, tail=bool(rng.integers(0, 2)))
+        g = seq.gate if rng.integers(0, 2) else rng.choice([-1, 0, 1], size=len(seq.gate))
+        P = int(rng.integers(0, 40))
+        want = mo.mtp_mask_dense(g, P)
+        assert np.array_equal(mo.mask_from_order(mo.mtp_codes(g, P), P), want)
