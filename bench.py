@@ -155,6 +155,60 @@ def cpu_baseline(cfg: dict, gate_cpu, reps: int, heads: int) -> dict:
                 threads=torch.get_num_threads(), cpu_count=os.cpu_count(), cpu_model=model)
 
 
+# bench phase -> kernel whose counters stand for it in the traffic summary
+PHASE_KERNEL = {"fwd": "attn_fwd_kernel", "bwd_dq_pass": "attn_bwd_dq_kernel",
+                "bwd_dkdv_pass": "attn_bwd_dkdv_kernel", "append_commit": "kv_copy_rows_kernel"}
+CALIB_ROWS = 65536   # rows per head of the calibration copy (8 heads x 256 B x 2 tensors = 268 MB)
+
+
+def load_traffic(path: str, config: int):
+    """HBM bytes per launch per kernel from a committed counter summary
+    (FETCH_SIZE + WRITE_SIZE scaled by the calibration copy), or None."""
+    try:
+        with open(path) as f:
+            t = json.load(f)
+    except (OSError, ValueError):
+        return None
+    if t.get("config") != config:
+        return None
+    return {k: v["traffic_bytes"] for k, v in t.get("kernels", {}).items()}
+
+
+def pmc_pass(torch, mga, libc, q, k, v, do, kp, cache, chunk0, P, S, R, Hkv, D, scale) -> int:
+    """One launch of each kernel for a hardware-counter run, preceded by a
+    calibration copy of known size (the append kernel, contiguous rows)."""
+    ops = mga.ops
+    dev = q.device
+    src = torch.randn(Hkv, CALIB_ROWS, D, device=dev).bfloat16()
+    dst_k = torch.empty_like(src)
+    dst_v = torch.empty_like(src)
+    torch.cuda.synchronize()
+    ops.kv_append(src, src, dst_k, dst_v, dst_offset=0)            # calibration copy
+    torch.cuda.synchronize()
+    L = P + S
+    kbuf, vbuf = cache.key_buffer(0), cache.value_buffer(0)
+    bm = mga.build_mtp_block_mask(chunk0["gate_mask"], P)
+    kbuf[:, P:L].copy_(k.detach()[0])     # torch copies: the append kernel runs only as
+    vbuf[:, P:L].copy_(v.detach()[0])     # the calibration copy and the commit below
+    kf, vf = kbuf[None, :, :L], vbuf[None, :, :L]
+    code, bmt = bm.mtp_code, bm.kernel_tensors()
+    qd = q.detach()
+    o, lse = ops.attn_fwd(qd, kf, vf, code, bmt, P, scale)
+    bufs = ops.bwd_buffers(qd, kf, P)
+    ops.attn_bwd(qd, kf, vf, o, lse, do, code, bmt, P, scale, P, passes=libc.BWD_DQ, buffers=bufs)
+    ops.attn_bwd(qd, kf, vf, o, lse, do, code, bmt, P, scale, P, passes=libc.BWD_DKDV, buffers=bufs)
+    idx, cnt = ops.regular_index(chunk0["regular_token_mask"])
+    app_k = torch.empty(Hkv, R + 16, D, dtype=torch.bfloat16, device=dev)
+    app_v = torch.empty_like(app_k)
+    ops.kv_append(k.detach(), v.detach(), app_k, app_v, dst_offset=0, idx=idx, n_rows=R)
+    torch.cuda.synchronize()
+    calib = Hkv * CALIB_ROWS * D * 2 * 2
+    print(json.dumps({"pmc_pass": True, "calibration": {"kernel": "kv_copy_rows_kernel",
+                                                        "read_bytes": calib, "write_bytes": calib,
+                                                        "grid_rows": CALIB_ROWS}}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -164,6 +218,11 @@ def main() -> int:
     ap.add_argument("--cpu-reps", type=int, default=3, help="timed runs of the CPU baseline (0 = skip)")
     ap.add_argument("--cpu-heads", type=int, default=4, help="query heads in the CPU sample (one KV group)")
     ap.add_argument("--phase-iters", type=int, default=20)
+    ap.add_argument("--pmc-pass", action="store_true",
+                    help="for hardware-counter runs: one known-size calibration copy, then one launch "
+                         "of each hot-path kernel; prints their byte counts and exits")
+    ap.add_argument("--traffic", default=str(ROOT / "profiles" / "config2_traffic.json"),
+                    help="counter summary (from rocprof_summary.py) that fills roofline.traffic")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -225,6 +284,9 @@ def main() -> int:
         mgr.past_seen_tokens = P
         return grads
 
+    if args.pmc_pass:
+        return pmc_pass(torch, mga, libc, q, k, v, do, kp, cache, chunk0, P, S, R, Hkv, D, scale)
+
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -278,6 +340,7 @@ def main() -> int:
 
     phases = {"mask_build": t_mask, "fwd": t_fwd, "bwd_dq_pass": t_dq, "bwd_dkdv_pass": t_dkdv,
               "append_commit": t_commit, "append_stage": t_stage}
+    traffic = load_traffic(args.traffic, args.config)
     credited = {"fwd": fl_fwd, "bwd_dq_pass": fl_dq, "bwd_dkdv_pass": fl_dkdv}
     dom = max(credited, key=lambda kname: phases[kname])
     attn_ms = t_fwd + t_dq + t_dkdv
@@ -302,7 +365,8 @@ def main() -> int:
                    "draft_length": cfg["draft"], "seed": SEED},
         "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(dom_tflops, 2),
                      "peak": PEAK_MFMA_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(dom_tflops / PEAK_MFMA_BF16_TFLOPS, 4), "traffic": None},
+                     "frac": round(dom_tflops / PEAK_MFMA_BF16_TFLOPS, 4),
+                     "traffic": traffic.get(PHASE_KERNEL[dom]) if traffic else None},
         "attention": {"credited_gflop": {"fwd": fl_fwd / 1e9, "bwd": (fl_dq + fl_dkdv) / 1e9,
                                          "total": fl_total / 1e9},
                       "tiles_area": {"prefix": a_pre, "chunk": a_cur},
@@ -315,6 +379,8 @@ def main() -> int:
                    "frac": round(commit_gbps / PEAK_HBM_GBPS, 4), "peak": PEAK_HBM_GBPS,
                    "stage_GBps": round(stage_bytes / (t_stage * 1e-3) / 1e9, 1)},
         "phases_ms": {kname: round(t, 5) for kname, t in phases.items()},
+        "hbm_traffic_bytes": ({PHASE_KERNEL[k_]: traffic.get(PHASE_KERNEL[k_]) for k_ in PHASE_KERNEL}
+                              if traffic else None),
         "host_ms_per_step": round(host_ms, 4),
     }
 

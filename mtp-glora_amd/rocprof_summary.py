@@ -1,0 +1,104 @@
+"""Summaries of rocprofv3 CSV output, written to profiles/.
+
+* ``stats``: a ``*_kernel_stats.csv`` (``--kernel-trace --stats``) as a
+  markdown table of per-kernel calls and average durations.
+* ``traffic``: two ``--pmc`` runs of ``bench.py --pmc-pass`` (one collecting
+  FETCH_SIZE, one WRITE_SIZE; both in KiB per dispatch) turned into HBM bytes
+  per launch for each kernel. Each counter is scaled by what it reads for the
+  pass's calibration copy, a ``kv_copy_rows_kernel`` dispatch that reads and
+  writes a known number of bytes (the largest-grid dispatch of that kernel).
+  Each kernel's figure is its last dispatch in the pass (the hot-path launch;
+  set-up work such as the prefix fill runs before it).
+
+    python mtp-glora_amd/rocprof_summary.py stats gpurun_out/prof/bench_kernel_stats.csv
+    python mtp-glora_amd/rocprof_summary.py traffic --fetch F.csv --write W.csv \\
+        --calib-read BYTES --calib-write BYTES --config 2 -o profiles/config2_traffic.json
+"""
+from __future__ import annotations
+
+import argparse
+import csv
+import json
+import re
+import sys
+
+CALIB_KERNEL = "kv_copy_rows_kernel"
+
+
+def kernel_base(name: str) -> str:
+    """``attn_fwd_kernel`` from a mangled or demangled kernel name."""
+    m = re.search(r"([a-z_]+_kernel)", name)
+    return m.group(1).lstrip("_") if m else name[:48]
+
+
+def stats_markdown(path: str) -> str:
+    rows = list(csv.DictReader(open(path)))
+    out = ["| Kernel | Calls | Avg (us) | Share |", "|---|---|---|---|"]
+    for r in rows:
+        out.append(f"| {kernel_base(r['Name'])} | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | "
+                   f"{float(r['Percentage']):.2f} % |")
+    return "\n".join(out)
+
+
+def _dispatches(path: str, counter: str):
+    """[(kernel, grid_size, KiB)] in dispatch order for one counter."""
+    out = []
+    for r in csv.DictReader(open(path)):
+        if r["Counter_Name"] != counter:
+            continue
+        out.append((kernel_base(r["Kernel_Name"]), int(r["Grid_Size"]), float(r["Counter_Value"]),
+                    int(r["Dispatch_Id"])))
+    out.sort(key=lambda t: t[3])
+    return out
+
+
+def traffic(fetch_csv: str, write_csv: str, calib_read: int, calib_write: int, config: int) -> dict:
+    result = {"config": config, "counters": ["FETCH_SIZE", "WRITE_SIZE"], "unit": "bytes per launch"}
+    scaled = {}
+    for counter, path, known in (("FETCH_SIZE", fetch_csv, calib_read), ("WRITE_SIZE", write_csv, calib_write)):
+        disp = _dispatches(path, counter)
+        calib = max((d for d in disp if d[0] == CALIB_KERNEL), key=lambda d: d[1])
+        factor = known / (calib[2] * 1024.0)
+        result[f"{counter}_calibration"] = {"known_bytes": known, "counter_KiB": calib[2], "factor": factor}
+        # the pass launches each hot-path kernel last (set-up copies come first)
+        last = {}
+        for d in disp:
+            if d is not calib:
+                last[d[0]] = d[2] * 1024.0 * factor
+        scaled[counter] = last
+    kernels = {}
+    for k in sorted(set(scaled["FETCH_SIZE"]) | set(scaled["WRITE_SIZE"])):
+        f = scaled["FETCH_SIZE"].get(k, 0.0)
+        w = scaled["WRITE_SIZE"].get(k, 0.0)
+        kernels[k] = {"fetch_bytes": round(f), "write_bytes": round(w), "traffic_bytes": round(f + w)}
+    result["kernels"] = kernels
+    return result
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    sub = ap.add_subparsers(dest="cmd", required=True)
+    s = sub.add_parser("stats")
+    s.add_argument("csv")
+    t = sub.add_parser("traffic")
+    t.add_argument("--fetch", required=True)
+    t.add_argument("--write", required=True)
+    t.add_argument("--calib-read", type=int, required=True)
+    t.add_argument("--calib-write", type=int, required=True)
+    t.add_argument("--config", type=int, default=2)
+    t.add_argument("-o", "--out")
+    args = ap.parse_args(argv)
+    if args.cmd == "stats":
+        print(stats_markdown(args.csv))
+        return 0
+    res = traffic(args.fetch, args.write, args.calib_read, args.calib_write, args.config)
+    text = json.dumps(res, indent=1)
+    if args.out:
+        with open(args.out, "w") as f:
+            f.write(text + "\n")
+    print(text)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

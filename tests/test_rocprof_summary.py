@@ -1,0 +1,39 @@
+"""The counter summary behind roofline.traffic: calibration by the copy of
+known size, last dispatch per kernel, kernel-name normalisation."""
+import csv
+import importlib
+
+rs = importlib.import_module("mtp-glora_amd.rocprof_summary")
+
+FIELDS = ["Dispatch_Id", "Grid_Size", "Kernel_Name", "Counter_Name", "Counter_Value"]
+
+
+def _write(path, counter, rows):
+    with open(path, "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=FIELDS)
+        w.writeheader()
+        for i, (name, grid, val) in enumerate(rows):
+            w.writerow(dict(Dispatch_Id=i + 1, Grid_Size=grid, Kernel_Name=name, Counter_Name=counter,
+                            Counter_Value=val))
+
+
+def test_traffic_calibration_and_last_dispatch(tmp_path):
+    f, w = tmp_path / "f.csv", tmp_path / "w.csv"
+    copy = "kv_copy_rows_kernel"
+    fwd = "_ZN3mga15attn_fwd_kernelILi1ELi128EDF16bEEvNS_8AttnArgsE"
+    # prefix fill (small copy), calibration (largest grid), attention, commit
+    _write(f, "FETCH_SIZE", [(copy, 100, 50.0), (copy, 1000, 512.0), (fwd, 10, 300.0), (copy, 80, 40.0)])
+    _write(w, "WRITE_SIZE", [(copy, 100, 100.0), (copy, 1000, 1024.0), (fwd, 10, 10.0), (copy, 80, 80.0)])
+    r = rs.traffic(str(f), str(w), calib_read=1024 * 1024, calib_write=1024 * 1024, config=2)
+    assert r["FETCH_SIZE_calibration"]["factor"] == 2.0
+    assert r["WRITE_SIZE_calibration"]["factor"] == 1.0
+    assert r["kernels"]["attn_fwd_kernel"] == {"fetch_bytes": 600 * 1024, "write_bytes": 10 * 1024,
+                                               "traffic_bytes": 610 * 1024}
+    # the commit (last dispatch), not the prefix fill
+    assert r["kernels"][copy]["fetch_bytes"] == 80 * 1024
+
+
+def test_kernel_base_names():
+    assert rs.kernel_base("_ZN3mga18attn_bwd_dq_kernelILi128EDF16bEEvNS_8AttnArgsE") == "attn_bwd_dq_kernel"
+    assert rs.kernel_base("void mga::attn_fwd_kernel<1, 128, float>(mga::AttnArgs)") == "attn_fwd_kernel"
+    assert rs.kernel_base("kv_copy_rows_kernel") == "kv_copy_rows_kernel"
