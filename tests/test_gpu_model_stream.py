@@ -1,0 +1,201 @@
+"""Config 1 end to end: a random-init Qwen3-style decoder (transformers'
+Qwen3ForCausalLM: 2 layers, hidden 256, 4 query / 2 KV heads, head_dim 64,
+vocab 1024, fp32) with Gated LoRA (rank 8) on q/k/v/o, trained over an MTP
+sequence in chunks exactly as the reference's chunk loop drives it
+(mtp_glora/trainer/trainer.py:95-136): reset -> per chunk prepare (BlockMask)
+-> forward with the cache -> loss.backward -> extract the regular-token K/V.
+
+The HIP path runs through the drop-in boundary only: the attention function
+registered with transformers, StreamingKVCache as past_key_values and
+StreamingKVCacheManager. It is checked against
+  * the reference's chunked procedure on the CPU in float64: the same model
+    with dense masked attention (the flex_attention semantics, the oracle's
+    MTP mask), transformers' DynamicCache, and the regular-token gather + cat +
+    detach of collator.py:270-287 between chunks -- forward logits and the
+    LoRA gradients accumulated over all chunks;
+  * a single pass over the whole sequence with the full MTP mask (forward
+    logits), the chunk-equivalence invariant: blocks never straddle chunks.
+Tolerance (bf16 MFMA arithmetic inside an fp32 model): logits max-abs 2e-2 and
+mean-abs 2e-3; LoRA gradients within 2e-2 of the largest reference entry
+(max) and 2e-3 of it (mean).
+"""
+import importlib
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import mtp_oracle as mo
+
+pytestmark = pytest.mark.gpu
+
+transformers = pytest.importorskip("transformers")
+from transformers import AttentionInterface, Qwen3Config, Qwen3ForCausalLM  # noqa: E402
+from transformers.cache_utils import DynamicCache  # noqa: E402
+
+N_REG, N_CHUNKS, N_ANCHOR, DRAFT, RANK, VOCAB = 1024, 4, 16, 4, 8, 1024
+MASK_ID = VOCAB - 1
+
+
+class GatedLoRA(torch.nn.Module):
+    """base(x) + s * B(A(x)) * gate, the gate being the chunk's clamped
+    gate_mask [1, S, 1] (1 on mask tokens with a label)."""
+
+    def __init__(self, base: torch.nn.Linear, rank: int, gen: torch.Generator):
+        super().__init__()
+        self.base = base
+        self.A = torch.nn.Parameter(torch.randn(rank, base.in_features, generator=gen) * 0.05)
+        self.B = torch.nn.Parameter(torch.randn(base.out_features, rank, generator=gen) * 0.05)
+        self.scale = 2.0
+        self.gate = None
+
+    def forward(self, x):
+        return self.base(x) + self.scale * ((x @ self.A.t()) @ self.B.t()) * self.gate
+
+
+def dense_masked_attention(module, query, key, value, attention_mask, scaling=None, dropout=0.0, **kw):
+    """flex_attention's dense semantics with a boolean [.., S, L] mask: GQA,
+    masked scores -inf, a fully masked row gives 0."""
+    G = query.shape[1] // key.shape[1]
+    k = key.repeat_interleave(G, dim=1)
+    v = value.repeat_interleave(G, dim=1)
+    s = (query @ k.transpose(-1, -2)) * scaling
+    m = attention_mask.bool()
+    s = s.masked_fill(~m, float("-inf"))
+    rowok = m.any(dim=-1, keepdim=True)
+    p = torch.softmax(s.masked_fill(~rowok, 0.0), dim=-1) * rowok
+    return (p @ v).transpose(1, 2).contiguous(), None
+
+
+def build_model(attn: str, dtype, device, seed: int = 0):
+    cfg = Qwen3Config(vocab_size=VOCAB, hidden_size=256, intermediate_size=512, num_hidden_layers=2,
+                      num_attention_heads=4, num_key_value_heads=2, head_dim=64,
+                      max_position_embeddings=4096, tie_word_embeddings=False)
+    cfg._attn_implementation = attn
+    torch.manual_seed(seed)
+    model = Qwen3ForCausalLM(cfg)
+    gen = torch.Generator().manual_seed(seed + 1)
+    loras = []
+    for layer in model.model.layers:
+        att = layer.self_attn
+        for name in ("q_proj", "k_proj", "v_proj", "o_proj"):
+            lo = GatedLoRA(getattr(att, name), RANK, gen)
+            setattr(att, name, lo)
+            loras.append(lo)
+    for p in model.parameters():
+        p.requires_grad_(False)
+    for lo in loras:
+        lo.A.requires_grad_(True)
+        lo.B.requires_grad_(True)
+    return model.to(device=device, dtype=dtype), loras
+
+
+def make_sequence(seed: int = 0):
+    """N_CHUNKS chunks of N_REG / N_CHUNKS regular tokens with N_ANCHOR anchors
+    each; token ids uniform from the seed, <mask> = MASK_ID; labels for the loss."""
+    rng = np.random.default_rng(seed)
+    per = N_REG // N_CHUNKS
+    chunks = []
+    for c in range(N_CHUNKS):
+        seq = mo.synth_sequence(per, mo.sample_anchors(per, N_ANCHOR, seed + c), DRAFT, pos0=c * per)
+        ids = rng.integers(0, VOCAB - 1, size=len(seq.gate))
+        ids[seq.regular == 0] = MASK_ID
+        labels = rng.integers(0, VOCAB - 1, size=len(seq.gate))
+        chunks.append((seq, ids, labels))
+    return chunks
+
+
+def chunk_loss(logits, labels):
+    return torch.nn.functional.cross_entropy(logits[0].float(), labels, reduction="sum") / labels.numel()
+
+
+def run_hip(mga, chunks, dev):
+    model, loras = build_model("mtp_hip", torch.float32, dev)
+    mgr = mga.StreamingKVCacheManager(capacity=4096)
+    mgr.reset_cache()
+    pkv = mgr.new_cache(num_layers=2)
+    logits_out = []
+    for c, (seq, ids, labels) in enumerate(chunks):
+        chunk = {"input_ids": torch.tensor(ids, device=dev)[None],
+                 "gate_mask": torch.tensor(seq.gate, device=dev)[None],
+                 "regular_token_mask": torch.tensor(seq.regular, device=dev)[None],
+                 "position_ids": torch.tensor(seq.position, device=dev)[None]}
+        chunk = mgr.prepare_data_with_kv_cache(chunk)
+        gate = chunk["gate_mask"].to(torch.float32)
+        for lo in loras:
+            lo.gate = gate
+        out = model(input_ids=chunk["input_ids"], attention_mask=chunk["attention_mask"],
+                    position_ids=chunk["position_ids"], past_key_values=pkv, use_cache=True)
+        chunk_loss(out.logits, torch.tensor(labels, device=dev)).backward()
+        logits_out.append(out.logits.detach().double().cpu())
+        if c + 1 < len(chunks):
+            pkv = mgr.extract_regular_kv_cache_for_next_chunk(chunk, out.past_key_values)
+    torch.cuda.synchronize()
+    grads = [torch.cat([lo.A.grad.flatten(), lo.B.grad.flatten()]).double().cpu() for lo in loras]
+    return logits_out, grads
+
+
+def run_reference(chunks):
+    model, loras = build_model("mtp_dense_ref", torch.float64, "cpu")
+    pkv = None
+    P = 0
+    logits_out = []
+    for c, (seq, ids, labels) in enumerate(chunks):
+        mask = torch.tensor(mo.mtp_mask_dense(seq.gate, P))[None, None]
+        gate = torch.tensor(seq.gate).clamp(min=0)[None, :, None].double()
+        for lo in loras:
+            lo.gate = gate
+        out = model(input_ids=torch.tensor(ids)[None], attention_mask=mask,
+                    position_ids=torch.tensor(seq.position)[None], past_key_values=pkv, use_cache=True)
+        chunk_loss(out.logits, torch.tensor(labels)).backward()
+        logits_out.append(out.logits.detach())
+        # collator.py:270-287: keep the regular rows, detached
+        idx = torch.tensor(np.nonzero(seq.regular)[0])
+        new = DynamicCache()
+        for li, layer in enumerate(out.past_key_values.layers):
+            k = torch.cat([layer.keys[:, :, :P], layer.keys[:, :, P:][:, :, idx]], dim=2).detach()
+            v = torch.cat([layer.values[:, :, :P], layer.values[:, :, P:][:, :, idx]], dim=2).detach()
+            new.update(k, v, li)
+        pkv = new
+        P += len(idx)
+    grads = [torch.cat([lo.A.grad.flatten(), lo.B.grad.flatten()]) for lo in loras]
+    return logits_out, grads
+
+
+def run_single_pass(chunks):
+    """One forward over the whole sequence with the full MTP mask."""
+    model, loras = build_model("mtp_dense_ref", torch.float64, "cpu")
+    gate_all = np.concatenate([s.gate for s, _, _ in chunks])
+    ids = np.concatenate([i for _, i, _ in chunks])
+    pos = np.concatenate([s.position for s, _, _ in chunks])
+    for lo in loras:
+        lo.gate = torch.tensor(gate_all).clamp(min=0)[None, :, None].double()
+    mask = torch.tensor(mo.mtp_mask_dense(gate_all, 0))[None, None]
+    with torch.no_grad():
+        out = model(input_ids=torch.tensor(ids)[None], attention_mask=mask,
+                    position_ids=torch.tensor(pos)[None], use_cache=False)
+    return torch.split(out.logits, [len(s.gate) for s, _, _ in chunks], dim=1)
+
+
+def _check(name, got, ref, max_abs, mean_abs):
+    err = (got - ref).abs()
+    print(f"  {name}: max-abs {err.max().item():.3e} mean-abs {err.mean().item():.3e}", flush=True)
+    assert err.max().item() <= max_abs and err.mean().item() <= mean_abs, name
+
+
+def test_config1_chunk_stream_through_transformers_qwen3(dev):
+    mga = importlib.import_module("mtp-glora_amd")
+    mga.register("mtp_hip")
+    AttentionInterface.register("mtp_dense_ref", dense_masked_attention)
+    chunks = make_sequence(0)
+    hip_logits, hip_grads = run_hip(mga, chunks, dev)
+    ref_logits, ref_grads = run_reference(chunks)
+    one_pass = run_single_pass(chunks)
+    for c in range(len(chunks)):
+        # chunk equivalence of the reference itself, then the HIP stream against both
+        assert torch.allclose(ref_logits[c], one_pass[c], atol=1e-9, rtol=0)
+        _check(f"logits chunk {c}", hip_logits[c], ref_logits[c], 2e-2, 2e-3)
+    for i, (g, r) in enumerate(zip(hip_grads, ref_grads)):
+        scale = r.abs().max().item()
+        assert scale > 0
+        _check(f"lora grad {i} (scale {scale:.2e})", g / scale, r / scale, 2e-2, 2e-3)
