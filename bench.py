@@ -52,6 +52,18 @@ CONFIGS = {
 }
 SEED = 1234
 
+# Chunk streams: per chunk (regular rows, anchors, draft length); every layer
+# runs update -> attention fwd -> bwd, then the regular rows are committed
+# (except after the last chunk, trainer.py:133).
+STREAMS = {
+    3: dict(workload="config3: Qwen3-8B, 36 layers, 8 chunks of 4096 regular + 512x4 mask rows, "
+                     "prefix 0 -> 28672",
+            Hq=32, Hkv=8, D=128, layers=36, chunks=[(4096, 512, 4)] * 8),
+    4: dict(workload="config4: Llama-3.1-8B, 32 layers, 32 chunks of 4096 regular + 256x4 mask rows "
+                     "to a 131072-token prefix, then a 768 regular + 64x4 mask (1024-row) remainder chunk",
+            Hq=32, Hkv=8, D=128, layers=32, chunks=[(4096, 256, 4)] * 32 + [(768, 64, 4)]),
+}
+
 
 def tile_areas(bm, S: int, L: int, P: int, block: int = 128):
     """(A_pre, A_cur): clipped areas of the non-empty tiles of the block mask,
@@ -209,12 +221,91 @@ def pmc_pass(torch, mga, libc, q, k, v, do, kp, cache, chunk0, P, S, R, Hkv, D, 
     return 0
 
 
+def stream_bench(torch, mga, syn, config: int, cfg: dict) -> int:
+    """Time one whole chunk stream (all layers, all chunks) through the
+    drop-in API after a one-chunk warm-up; credited FLOPs per chunk from that
+    chunk's block mask, times the layer count."""
+    dev = torch.device("cuda:0")
+    Hq, Hkv, D, nl = cfg["Hq"], cfg["Hkv"], cfg["D"], cfg["layers"]
+    scale = D ** -0.5
+    chunks, P = [], 0
+    for c, (n_reg, n_anchor, draft) in enumerate(cfg["chunks"]):
+        anchors = syn.sample_anchors(n_reg, n_anchor, SEED + c)
+        chunks.append(syn.mtp_chunk(n_reg, anchors, draft, pos0=P, device=dev, seed=SEED + c))
+        P += n_reg
+    Smax = max(ch["gate_mask"].shape[1] for ch in chunks)
+    cap = P + Smax + 256
+    g = torch.Generator(device=dev).manual_seed(SEED)
+    rnd = lambda shape, sd: (torch.randn(*shape, generator=g, device=dev) * sd).bfloat16()
+    # one set of projections per chunk length, shared by the layers (values do not affect time)
+    tens = {}
+    for ch in chunks:
+        S = ch["gate_mask"].shape[1]
+        if S not in tens:
+            tens[S] = (rnd((1, S, Hq, D), 0.5).transpose(1, 2).requires_grad_(),
+                       rnd((1, S, Hkv, D), 0.5).transpose(1, 2).requires_grad_(),
+                       rnd((1, S, Hkv, D), 0.5).transpose(1, 2).requires_grad_(),
+                       rnd((1, S, Hq, D), 1.0))
+    mgr = mga.StreamingKVCacheManager(capacity=cap, sanity_check=False)
+    module = torch.nn.Module()
+
+    def run(nchunks):
+        mgr.reset_cache()
+        cache = mgr.new_cache(num_layers=nl)
+        for c in range(nchunks):
+            chunk = mgr.prepare_data_with_kv_cache(dict(chunks[c]))
+            q, k, v, do = tens[chunk["input_ids"].shape[1]]
+            for layer in range(nl):
+                kf, vf = cache.update(k, v, layer)
+                o, _ = mga.mtp_attention_forward(module, q, kf, vf, chunk["attention_mask"], scaling=scale)
+                torch.autograd.grad(o, (q, k, v), do)
+            if c + 1 < len(chunks):
+                cache = mgr.extract_regular_kv_cache_for_next_chunk(chunk, cache)
+
+    run(1)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    run(len(chunks))
+    e1.record()
+    torch.cuda.synchronize()
+    host_s = time.perf_counter() - t0
+    seconds = e0.elapsed_time(e1) / 1e3
+
+    credited, append_bytes, P = 0, 0, 0
+    for c, ch in enumerate(chunks):
+        S = ch["gate_mask"].shape[1]
+        bm = mga.build_mtp_block_mask(ch["gate_mask"], P)
+        a_pre, a_cur = tile_areas(bm, S, P + S, P)
+        credited += nl * Hq * D * (4 * (a_pre + a_cur) + 6 * a_pre + 10 * a_cur)
+        R = int(ch["regular_token_mask"].sum())
+        if c + 1 < len(chunks):
+            append_bytes += nl * 2 * R * Hkv * D * 2 * 2
+        P += R
+    tflops = credited / seconds / 1e12
+    out = {
+        "metric": METRIC, "value": round(tflops, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": 1,
+        "warmup": 1, "ms_per_step": round(seconds * 1e3, 2), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": cfg["workload"], "Hq": Hq, "Hkv": Hkv, "head_dim": D, "layers": nl,
+                   "chunks": len(chunks), "final_prefix": P, "seed": SEED},
+        "stream": {"credited_tflop": round(credited / 1e12, 2), "seconds": round(seconds, 4),
+                   "host_seconds": round(host_s, 4), "append_bytes": append_bytes,
+                   "roofline_frac": round(tflops / PEAK_MFMA_BF16_TFLOPS, 4),
+                   "step": "per chunk: block mask; per layer: cache update, attention fwd, bwd; "
+                           "then the regular-row commit of every layer (not after the last chunk)"},
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", type=int, default=2, choices=sorted(CONFIGS))
+    ap.add_argument("--config", type=int, default=2, choices=sorted(set(CONFIGS) | set(STREAMS)))
     ap.add_argument("--cpu-reps", type=int, default=3, help="timed runs of the CPU baseline (0 = skip)")
     ap.add_argument("--cpu-heads", type=int, default=4, help="query heads in the CPU sample (one KV group)")
     ap.add_argument("--phase-iters", type=int, default=20)
@@ -243,6 +334,9 @@ def main() -> int:
     mga.load_library()
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+
+    if args.config in STREAMS:
+        return stream_bench(torch, mga, syn, args.config, STREAMS[args.config])
 
     cfg = CONFIGS[args.config]
     Hq, Hkv, D, P = cfg["Hq"], cfg["Hkv"], cfg["D"], cfg["P"]
