@@ -174,6 +174,39 @@ __device__ __forceinline__ TrLane tr_lane(int lane) {
   return t;
 }
 
+// A lane offset whose bits the compiler may not reason about. Added to an LDS
+// buffer's address it stays an add, so the buffer base and constant parts fold
+// into the ds_read offset field; with known-disjoint bits the add becomes an
+// or, and every (buffer, offset) pair costs a register.
+__device__ __forceinline__ uint32_t opaque_u32(uint32_t x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
+__device__ __forceinline__ const char *lds_at(const void *base, uint32_t byte_off) {
+  return reinterpret_cast<const char *>(base) + byte_off;
+}
+
+// Byte offsets of the transposed operand reads (see TrLane) for every 32-column
+// block: the tile base and the k0 row term are added as constants.
+template <int HD>
+struct TrOffsets {
+  uint32_t off[2][HD / 32];
+  __device__ __forceinline__ void init(int lane) {
+    const TrLane t = tr_lane<HD>(lane);
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int mb = 0; mb < HD / 32; ++mb)
+        off[s][mb] = opaque_u32((uint32_t)(t.row[s] * HD + t.lo[s] + ((mb ^ t.hi2[s]) << 5)) * 2u);
+  }
+  __device__ __forceinline__ bf16x8 operand(const bf16_t *tile, int k0, int mblk) const {
+    const char *b = reinterpret_cast<const char *>(tile) + k0 * HD * 2;
+    return join8(lds_tr4(reinterpret_cast<const bf16_t *>(b + off[0][mblk])),
+                 lds_tr4(reinterpret_cast<const bf16_t *>(b + off[1][mblk])));
+  }
+};
+
 template <int HD>
 __device__ __forceinline__ bf16x8 lds_tr_operand(const bf16_t *tile, const TrLane &t, int k0, int mblk) {
   const bf16_t *p0 = tile + (k0 + t.row[0]) * HD + t.lo[0] + ((mblk ^ t.hi2[0]) << 5);
@@ -226,7 +259,7 @@ __device__ __forceinline__ void tile_dma(bf16_t *tile, const bf16_t *src, int64_
   constexpr int kGranRow = HD / 8;                 // granules per row
   constexpr int kRowsPerInst = 64 / kGranRow;      // rows per 1 KB block
   constexpr int kInst = NR / kRowsPerInst / 4;     // blocks per wave
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int p = lane % kGranRow;
 #pragma unroll
   for (int i = 0; i < kInst; ++i) {
@@ -282,29 +315,41 @@ __device__ __forceinline__ int key_w(const int32_t *code, int key, int P, int L)
 
 __device__ __forceinline__ int query_v(int qcode) { return qcode == kCodeX ? kWX : qcode; }
 
-// Per-lane element offsets of the direct loads of an NR x HD tile whose rows
-// are r0 .. r0 + NR - 1 of a source with row stride ss (see tile_dma). With
-// these the load address is a wave-uniform row base plus a lane constant.
+// The wave's index within the workgroup as a scalar (wave-uniform) value, so
+// LDS block bases derived from it stay in scalar registers.
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
+
+// Per-lane offsets of the direct loads of an NR x HD tile (see tile_dma). Load
+// i of wave w covers tile rows (w * kInst + i) * kRowsPerInst + lane / kGranRow:
+// the wave-uniform part of that row goes into the scalar base address, the
+// lane's row term (lrow, bytes) and granule term (gran[i], bytes; the swizzle
+// is linear in the row bits, so it splits into a lane part and an i part)
+// into the 32-bit vector offset. gran does not depend on the row stride, so
+// tiles of different sources share it.
 template <int HD, int NR>
 struct DmaLane {
   static constexpr int kGranRow = HD / 8;
   static constexpr int kRowsPerInst = 64 / kGranRow;
   static constexpr int kInst = NR / kRowsPerInst / 4;
-  uint32_t off[kInst];   // bytes
-  __device__ __forceinline__ void init(int64_t ss) {
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  uint32_t gran[kInst];
+  __device__ __forceinline__ void init() {
+    const int lane = threadIdx.x & 63, w = wave_id();
     const int p = lane % kGranRow;
 #pragma unroll
     for (int i = 0; i < kInst; ++i) {
       const int r = (w * kInst + i) * kRowsPerInst + lane / kGranRow;
-      off[i] = (uint32_t)(r * ss * 2) + (uint32_t)((p ^ swz<HD>(r)) << 4);
+      gran[i] = opaque_u32((uint32_t)((p ^ swz<HD>(r)) << 4));
     }
+  }
+  // byte offset of the lane's row within a load's row block, for row stride ss
+  __device__ __forceinline__ static uint32_t lane_row(int64_t ss) {
+    return opaque_u32((uint32_t)(((threadIdx.x & 63) / kGranRow) * ss * 2));
   }
   // only rows 0 .. nvalid - 1 of the tile exist, 1 <= nvalid < NR (callers
   // issue nothing for a tile with no rows): later rows repeat the last one
   __device__ __forceinline__ void issue_clamped(bf16_t *tile, const bf16_t *rowbase, int64_t ss,
                                                 int nvalid) const {
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, w = wave_id();
     const int p = lane % kGranRow;
     const char *base = reinterpret_cast<const char *>(rowbase);
 #pragma unroll
@@ -315,12 +360,15 @@ struct DmaLane {
     }
   }
   // rows r0 .. r0 + NR - 1 all exist in the source; rowbase is wave-uniform
-  __device__ __forceinline__ void issue(bf16_t *tile, const bf16_t *rowbase) const {
-    const int w = threadIdx.x >> 6;
-    const char *base = reinterpret_cast<const char *>(rowbase);
+  __device__ __forceinline__ void issue(bf16_t *tile, const bf16_t *rowbase, int64_t ss, uint32_t lrow) const {
+    const int w = wave_id();
 #pragma unroll
-    for (int i = 0; i < kInst; ++i)
-      __builtin_amdgcn_global_load_lds(base + off[i], (lds_void *)(tile + (w * kInst + i) * 512), 16, 0, 0);
+    for (int i = 0; i < kInst; ++i) {
+      const char *blk = reinterpret_cast<const char *>(rowbase + (int64_t)((w * kInst + i) * kRowsPerInst) * ss);
+      // formed at the use: hoisted out of a loop, the sums would hold registers
+      const uint32_t vo = opaque_u32(lrow) + gran[i];
+      __builtin_amdgcn_global_load_lds(blk + vo, (lds_void *)(tile + (w * kInst + i) * 512), 16, 0, 0);
+    }
   }
 };
 

@@ -16,11 +16,17 @@
 // NB = 2: 64 rows per wave, 1 wave per SIMD; every K and V^T operand read from
 // LDS feeds two MFMAs and the larger register budget keeps reads in flight.
 //
-// Rescaling of O is lazy: the running max only moves when a new score exceeds
-// it by more than 2^8 (log2 domain), which keeps every probability below 256
-// and leaves the result exact up to rounding (the final normalisation uses the
-// same max). Masking on partial tiles is one ordered compare per score (see
-// key_w) plus the causal bound on the steps that cross the diagonal.
+// Softmax without a per-step row max: probabilities are exp2(s * c - m) with
+// m the row's running offset, and a step is accepted when every lane's partial
+// row sum is at most 2^20 (so is every probability). Otherwise (a row's first
+// unmasked scores, or a score more than 20 log2 units above m) the step takes
+// the slow path: m moves to the exact running max, O and the row sum are
+// rescaled and the probabilities recomputed from the scores still held in
+// registers. Row sums are taken from the bf16-rounded probabilities the O
+// update multiplies (v_dot2), so the normalisation matches the weights used.
+// Masking is compiled only into the partial-tile variant of a step: one
+// ordered compare per score (see key_w) plus the causal bound when the step
+// crosses the diagonal.
 // Semantics: [torch]_higher_order_ops/flex_attention.py:202-267 (masked
 // scores -inf; a fully masked row has output 0 and LSE -inf).
 #include <type_traits>
@@ -33,10 +39,26 @@ namespace mga {
 namespace {
 
 constexpr float kNegInfF = -__builtin_huge_valf();
-constexpr float kLazyMax = 8.0f;   // log2-domain slack before O is rescaled
+constexpr float kPBound = 1048576.f;   // 2^20: largest partial row sum of a step on the fast path
 constexpr int kStepKeys = 64;
 
+typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2;
+
 __device__ __forceinline__ float exp2f_(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// two probabilities -> one packed bf16 pair (round to nearest even)
+__device__ __forceinline__ uint32_t cvt2(float x, float y) {
+  bf16x2 v;
+  v[0] = (bf16_t)x;
+  v[1] = (bf16_t)y;
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// acc + the two bf16 values of p
+__device__ __forceinline__ float add_pair(uint32_t p, float acc) {
+  const bf16x2 one = {(bf16_t)1.0f, (bf16_t)1.0f};
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, p), one, acc, false);
+}
 
 // Heads sharing a workgroup (a divisor of both G and 4).
 __host__ __device__ __forceinline__ int heads_per_wg(int G) { return (G % 4 == 0) ? 4 : (G % 2 == 0 ? 2 : 1); }
@@ -98,14 +120,19 @@ __global__ __launch_bounds__(256, 3 - NB) void attn_fwd_kernel(AttnArgs a) {
   auto step_base = [&](int j) { return tiles.at(j >> 1) * kBlock + (j & 1) * kStepKeys; };
 
   // per-lane LDS offsets: K rows (A operand of QK^T) and the V^T transpose reads
-  const int krow_sw = swz<HD>(l32);
-  const TrLane tl = tr_lane<HD>(lane);
+  // K operand of k-step ks: row l32 (+ 32 kb), granule (2 ks + hi) ^ swz(l32),
+  // i.e. byte offset krow ^ (ks << 5)
+  const uint32_t krow = opaque_u32((uint32_t)(l32 * HD + (((uint32_t)hi ^ swz<HD>(l32)) << 3)) * 2u);
+  TrOffsets<HD> tro;
+  tro.init(lane);
 
   constexpr bool kDirect = sizeof(T) == 2;
-  DmaLane<HD, kStepKeys> dmaK, dmaV;
+  DmaLane<HD, kStepKeys> dma;   // shared by the K and V tiles
+  uint32_t lrowK = 0, lrowV = 0;
   if constexpr (kDirect) {
-    dmaK.init(a.k_ss);
-    dmaV.init(a.v_ss);
+    dma.init();
+    lrowK = dma.lane_row(a.k_ss);
+    lrowV = dma.lane_row(a.v_ss);
   }
   TileStage<HD, kDirect ? 0 : kStepKeys, T> stK, stV;
   KeyCode wkey;
@@ -115,11 +142,11 @@ __global__ __launch_bounds__(256, 3 - NB) void attn_fwd_kernel(AttnArgs a) {
       if (kb >= a.L) {
         // second half of the last tile, past the keys: never computed, nothing to load
       } else if (kb + kStepKeys <= a.L) {
-        dmaK.issue(dK, reinterpret_cast<const bf16_t *>(kp) + (int64_t)kb * a.k_ss);
-        dmaV.issue(dV, reinterpret_cast<const bf16_t *>(vp) + (int64_t)kb * a.v_ss);
+        dma.issue(dK, reinterpret_cast<const bf16_t *>(kp) + (int64_t)kb * a.k_ss, a.k_ss, lrowK);
+        dma.issue(dV, reinterpret_cast<const bf16_t *>(vp) + (int64_t)kb * a.v_ss, a.v_ss, lrowV);
       } else {
-        dmaK.issue_clamped(dK, reinterpret_cast<const bf16_t *>(kp) + (int64_t)kb * a.k_ss, a.k_ss, a.L - kb);
-        dmaV.issue_clamped(dV, reinterpret_cast<const bf16_t *>(vp) + (int64_t)kb * a.v_ss, a.v_ss, a.L - kb);
+        dma.issue_clamped(dK, reinterpret_cast<const bf16_t *>(kp) + (int64_t)kb * a.k_ss, a.k_ss, a.L - kb);
+        dma.issue_clamped(dV, reinterpret_cast<const bf16_t *>(vp) + (int64_t)kb * a.v_ss, a.v_ss, a.L - kb);
       }
     } else {
       stK.load(kp, a.k_ss, kb, a.L - 1);
@@ -135,15 +162,15 @@ __global__ __launch_bounds__(256, 3 - NB) void attn_fwd_kernel(AttnArgs a) {
       stK.store(dK);
       stV.store(dV);
     }
-    if (tid < kStepKeys) dW[tid] = wkey.w();
+    if (tid < kStepKeys) *reinterpret_cast<int *>(const_cast<char *>(lds_at(dW, opaque_u32(tid * 4u)))) = wkey.w();
   };
 
-  float m_run[NB], m_use[NB], l_run[NB];
+  const float c = a.scale_log2;
+  float m_run[NB], l_run[NB];
   f32x16 oacc[NB][DB];
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
-    m_run[nb] = kNegInfF;
-    m_use[nb] = 0.f;
+    m_run[nb] = qlim[nb] < 0 ? 0.f : kNegInfF;   // a pad row never needs an offset
     l_run[nb] = 0.f;
 #pragma unroll
     for (int db = 0; db < DB; ++db) oacc[nb][db] = zero16();
@@ -158,9 +185,9 @@ __global__ __launch_bounds__(256, 3 - NB) void attn_fwd_kernel(AttnArgs a) {
     const bool partial = (j >> 1) < npart;
     if (j + 1 < nstep) load_step(j + 1, B ? sK0 : sK1, B ? sV0 : sV1);
 
+    // S^T = K Q^T for 64 keys x WR queries; register r of sacc[kb][nb] is key
+    // kb * 32 + 8 (r / 4) + 4 hi + r % 4 of the step, query row block nb.
     if (kbase < a.L) {
-      // S^T = K Q^T for 64 keys x WR queries; register r of sacc[kb][nb] is key
-      // kb * 32 + 8 (r / 4) + 4 hi + r % 4 of the step, query row block nb
       f32x16 sacc[2][NB];
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
@@ -170,7 +197,8 @@ __global__ __launch_bounds__(256, 3 - NB) void attn_fwd_kernel(AttnArgs a) {
       for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
-          const bf16x8 af = lds_read8(tK + (kb * 32 + l32) * HD + (((2 * ks + hi) ^ krow_sw) << 3));
+          const bf16x8 af = lds_read8(reinterpret_cast<const bf16_t *>(
+              lds_at(tK + kb * 32 * HD, krow ^ (uint32_t)(ks << 5))));
 #pragma unroll
           for (int nb = 0; nb < NB; ++nb) sacc[kb][nb] = mfma32(af, qf[nb][ks], sacc[kb][nb]);
         }
@@ -178,8 +206,9 @@ __global__ __launch_bounds__(256, 3 - NB) void attn_fwd_kernel(AttnArgs a) {
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) {
         if (partial) {
+          // a real branch: if-converted, full tiles would pay for the masking
+          asm volatile("");
           const int lim = qlim[nb] - kbase - 4 * hi;   // key offset (without 4 hi) must be <= lim
-          const bool diag = __builtin_amdgcn_ballot_w64(lim < kStepKeys - 1) != 0;
 #pragma unroll
           for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -187,22 +216,42 @@ __global__ __launch_bounds__(256, 3 - NB) void attn_fwd_kernel(AttnArgs a) {
               const i32x4 w4 = *reinterpret_cast<const i32x4 *>(&tW[kb * 32 + 8 * i + 4 * hi]);
 #pragma unroll
               for (int e = 0; e < 4; ++e) {
-                bool ok = w4[e] >= qv[nb];
-                if (diag) ok = ok & (kb * 32 + 8 * i + e <= lim);
+                const bool ok = (w4[e] >= qv[nb]) & (kb * 32 + 8 * i + e <= lim);
                 sacc[kb][nb][4 * i + e] = ok ? sacc[kb][nb][4 * i + e] : kNegInfF;
               }
             }
         }
-        // running max with lazy rescale: m moves only when a score exceeds it by 2^8
-        float mx = kNegInfF;
+        // probabilities against the running offset; the slow path when a
+        // partial row sum leaves the bound (or the row had no offset yet)
+        auto probs = [&](float m) {
+          float ps = 0.f;
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
+          for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kb][nb][r]);
-        mx = fmaxf(mx, xor32(mx)) * a.scale_log2;
-        if (__builtin_amdgcn_ballot_w64(mx > m_run[nb] + kLazyMax)) {
+            for (int u = 0; u < 2; ++u) {
+              i32x4 wv;
+#pragma unroll
+              for (int t = 0; t < 4; ++t) {
+                const float p0 = exp2f_(__builtin_fmaf(sacc[kb][nb][8 * u + 2 * t], c, -m));
+                const float p1 = exp2f_(__builtin_fmaf(sacc[kb][nb][8 * u + 2 * t + 1], c, -m));
+                const uint32_t w = cvt2(p0, p1);
+                wv[t] = (int)w;
+                ps = add_pair(w, ps);
+              }
+              pb[nb][2 * kb + u] = __builtin_bit_cast(bf16x8, wv);
+            }
+          return ps;
+        };
+        float ps = probs(m_run[nb]);
+        if (__builtin_amdgcn_ballot_w64(!(ps <= kPBound))) {
+          float mx = kNegInfF;
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kb][nb][r]);
+          mx = fmaxf(mx, xor32(mx)) * c;
           const float m_new = fmaxf(m_run[nb], mx);
-          if (m_new != m_run[nb]) {
+          if (m_new > m_run[nb]) {
             const float alpha = exp2f_(m_run[nb] - m_new);   // 0 when m_run = -inf
             l_run[nb] *= alpha;
 #pragma unroll
@@ -211,34 +260,18 @@ __global__ __launch_bounds__(256, 3 - NB) void attn_fwd_kernel(AttnArgs a) {
               for (int r = 0; r < 16; ++r) oacc[nb][db][r] *= alpha;
             m_run[nb] = m_new;
           }
-          m_use[nb] = m_run[nb] == kNegInfF ? 0.f : m_run[nb];
-        }
-        float ps = 0.f;
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const float p = exp2f_(__builtin_fmaf(sacc[kb][nb][r], a.scale_log2, -m_use[nb]));
-            sacc[kb][nb][r] = p;
-            ps += p;
-          }
-#pragma unroll
-          for (int u = 0; u < 2; ++u) {
-            const f32x16 &s = sacc[kb][nb];
-            pb[nb][2 * kb + u] = pack8(s[8 * u + 0], s[8 * u + 1], s[8 * u + 2], s[8 * u + 3],
-                                       s[8 * u + 4], s[8 * u + 5], s[8 * u + 6], s[8 * u + 7]);
-          }
+          ps = probs(m_run[nb] == kNegInfF ? 0.f : m_run[nb]);
         }
         l_run[nb] += ps;
       }
       // O^T += V^T P^T (each V^T operand serves the NB row blocks)
 #pragma unroll
-      for (int c = 0; c < 4; ++c)
+      for (int cc = 0; cc < 4; ++cc)
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
-          const bf16x8 va = lds_tr_operand<HD>(tV, tl, c * 16, db);
+          const bf16x8 va = tro.operand(tV, cc * 16, db);
 #pragma unroll
-          for (int nb = 0; nb < NB; ++nb) oacc[nb][db] = mfma32(va, pb[nb][c], oacc[nb][db]);
+          for (int nb = 0; nb < NB; ++nb) oacc[nb][db] = mfma32(va, pb[nb][cc], oacc[nb][db]);
         }
     }
 
