@@ -2,9 +2,8 @@
 //
 // Same work decomposition as the forward (mga_fwd.hip): a workgroup of 4 waves
 // holds 4 (query head, 32-row block) pairs of one kv head, so each staged K/V
-// tile feeds four heads. Q stays in registers; each lane parks its dO row in
-// LDS (read back only by itself: register relief that costs no memory wait).
-// Per 32-key step each wave computes
+// tile feeds four heads. Q and dO stay in registers. Per 32-key step each
+// wave computes
 //   S^T  = K Q^T,  dP^T = V dO^T                    (A operands: K, V rows)
 //   P    = exp2(S^T * scale_log2 - lse_log2)         (0 where masked)
 //   dS^T = P (dP^T - delta)
@@ -61,7 +60,6 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) bf16_t sK0[TILE], sK1[TILE];
   __shared__ __attribute__((aligned(16))) bf16_t sV0[TILE], sV1[TILE];
   __shared__ __attribute__((aligned(16))) int sW0[kStep], sW1[kStep];
-  __shared__ __attribute__((aligned(16))) bf16_t sDO[4][32 * HD];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, hi = lane >> 5;
@@ -88,15 +86,12 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnArgs a) {
   const T *kp = reinterpret_cast<const T *>(a.k) + g * a.k_sh;
   const T *vp = reinterpret_cast<const T *>(a.v) + g * a.v_sh;
 
-  // Q fragments in registers; this lane's dO half-row granules to its own LDS row
-  const int krow_sw = swz<HD>(l32);
-  bf16_t *myDO = sDO[wave];
-  bf16x8 qf[KS];
+  // Q and dO fragments (B operands of S^T and dP^T) in registers
+  bf16x8 qf[KS], dof[KS];
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
     qf[ks] = load8(qp + ks * 16 + hi * 8);
-    *reinterpret_cast<i32x4 *>(myDO + l32 * HD + (((2 * ks + hi) ^ krow_sw) << 3)) =
-        __builtin_bit_cast(i32x4, load8(dop + ks * 16 + hi * 8));
+    dof[ks] = load8(dop + ks * 16 + hi * 8);
   }
   float del = half_row_dot<HD, T>(op, dop, hi);
   del += xor32(del);
@@ -105,6 +100,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnArgs a) {
   const float lse = in ? a.lse[(int64_t)h * a.S + row] : kNegInfD;
   // a fully masked row has LSE -inf: it reaches no key (qlim = -1) and its P is 0
   const float lse2 = lse == kNegInfD ? 0.f : lse * kLog2e;
+  const float c = a.scale_log2;
   const int qcode = in ? a.code[row] : kCodePad;
   const int qv = query_v(qcode);
   const int qlim = (qcode == kCodePad || lse == kNegInfD) ? -1 : row + a.P;
@@ -116,7 +112,11 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnArgs a) {
   const int nstep = kSub * ntot;
   auto step_base = [&](int j) { return tiles.at(j / kSub) * kBlock + (j % kSub) * kStep; };
 
-  const TrLane tl = tr_lane<HD>(lane);
+  // K / V / dO operand of k-step ks: row l32, granule (2 ks + hi) ^ swz(l32),
+  // i.e. byte offset krow ^ (ks << 5); K^T through the transpose reads
+  const uint32_t krow = opaque_u32((uint32_t)(l32 * HD + (((uint32_t)hi ^ swz<HD>(l32)) << 3)) * 2u);
+  TrOffsets<HD> tro;
+  tro.init(lane);
 
   // bf16 operands go global -> LDS directly (no staging registers); fp32
   // operands are converted through registers.
@@ -143,7 +143,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnArgs a) {
     } else {
       __builtin_amdgcn_s_waitcnt(0);   // this thread's direct loads have landed
     }
-    if (tid < kStep) dW[tid] = knext.w();
+    if (tid < kStep) *reinterpret_cast<int *>(const_cast<char *>(lds_at(dW, opaque_u32(tid * 4u)))) = knext.w();
   };
 
   f32x16 dqacc[DB];
@@ -168,28 +168,26 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnArgs a) {
       for (int r = 0; r < 16; ++r) dpacc[r] = -del;
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        const int off = l32 * HD + (((2 * ks + hi) ^ krow_sw) << 3);
-        sacc = mfma32(lds_read8(tK + off), qf[ks], sacc);
-        dpacc = mfma32(lds_read8(tV + off), lds_read8(myDO + off), dpacc);
+        const uint32_t off = krow ^ (uint32_t)(ks << 5);
+        sacc = mfma32(lds_read8(reinterpret_cast<const bf16_t *>(lds_at(tK, off))), qf[ks], sacc);
+        dpacc = mfma32(lds_read8(reinterpret_cast<const bf16_t *>(lds_at(tV, off))), dof[ks], dpacc);
       }
-      const int lim = qlim - kbase - 4 * hi;   // causal: key offset (without 4 hi) <= lim
-      const bool diag = partial && __builtin_amdgcn_ballot_w64(lim < kStep - 1) != 0;
+      if (partial) {
+        // a real branch: if-converted, full tiles would pay for the masking
+        asm volatile("");
+        const int lim = qlim - kbase - 4 * hi;   // causal: key offset (without 4 hi) <= lim
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        i32x4 w4 = {kWX, kWX, kWX, kWX};
-        if (partial) w4 = *reinterpret_cast<const i32x4 *>(&tW[8 * i + 4 * hi]);
+        for (int i = 0; i < 4; ++i) {
+          const i32x4 w4 = *reinterpret_cast<const i32x4 *>(&tW[8 * i + 4 * hi]);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int r = 4 * i + e;
-          float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[r], a.scale_log2, -lse2));
-          if (partial) {
-            bool ok = w4[e] >= qv;
-            if (diag) ok = ok & (8 * i + e <= lim);
-            p = ok ? p : 0.f;
+          for (int e = 0; e < 4; ++e) {
+            const bool ok = (w4[e] >= qv) & (8 * i + e <= lim);
+            sacc[4 * i + e] = ok ? sacc[4 * i + e] : kNegInfD;   // P = exp2(-inf) = 0
           }
-          dpacc[r] = p * dpacc[r];
         }
       }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) dpacc[r] *= __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[r], c, -lse2));
       // dQ^T += K^T dS^T
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
@@ -197,7 +195,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnArgs a) {
                                  dpacc[8 * u + 4], dpacc[8 * u + 5], dpacc[8 * u + 6], dpacc[8 * u + 7]);
 #pragma unroll
         for (int db = 0; db < DB; ++db)
-          dqacc[db] = mfma32(lds_tr_operand<HD>(tK, tl, 16 * u, db), dsb, dqacc[db]);
+          dqacc[db] = mfma32(tro.operand(tK, 16 * u, db), dsb, dqacc[db]);
       }
     }
 
