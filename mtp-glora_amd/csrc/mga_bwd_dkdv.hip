@@ -26,6 +26,16 @@ namespace {
 constexpr float kNegInfK = -__builtin_huge_valf();
 constexpr int kQStep = 64;
 
+typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2;
+
+// two values -> one packed bf16 pair (round to nearest even)
+__device__ __forceinline__ uint32_t cvt2(float x, float y) {
+  bf16x2 v;
+  v[0] = (bf16_t)x;
+  v[1] = (bf16_t)y;
+  return __builtin_bit_cast(uint32_t, v);
+}
+
 }  // namespace
 
 template <int HD, typename T>
@@ -78,8 +88,13 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(AttnArgs a, int k
   const int nstep = 2 * ntot;
   auto step_base = [&](int j) { return tiles.at(j >> 1) * kBlock + (j & 1) * kQStep; };
 
-  const int qrow_sw = swz<HD>(l32);
-  const TrLane tl = tr_lane<HD>(lane);
+  // Q / dO operand of k-step ks for 32-row block qb: row qb * 32 + l32,
+  // granule (2 ks + hi) ^ swz(l32), i.e. byte offset qrow ^ (ks << 5);
+  // Q^T and dO^T through the transpose reads
+  const uint32_t qrow = opaque_u32((uint32_t)(l32 * HD + (((uint32_t)hi ^ swz<HD>(l32)) << 3)) * 2u);
+  TrOffsets<HD> tro;
+  tro.init(lane);
+  const float c = a.scale_log2;
 
   constexpr bool kDirect = sizeof(T) == 2;
   TileStage<HD, kDirect ? 0 : kQStep, T> stQ, stD;
@@ -139,51 +154,86 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(AttnArgs a, int k
     const bool partial = (j >> 1) < npart;
     if (j + 1 < nstep) load_step(j + 1, B ? sQ0 : sQ1, B ? sD0 : sD1);
 
-    if (q0 < a.S) {
+    // Program order is the schedule. A step is 4 blocks of 2 KS MFMAs:
+    //   0: S / dP of rows 0..31,  1: S / dP of rows 32..63 (+ softmax of 0..31),
+    //   2: dV / dK update of rows 0..31 (+ softmax of 32..63),  3: update of 32..63.
+    // Every LDS operand is read kAhead MFMAs before its use (a ring of
+    // registers) and a scheduling fence closes each MFMA slot, so the compiler
+    // neither hoists all reads nor leaves a read next to its use. MASKED: a
+    // partial tile (masking compiled in; a full tile's step has none).
+    auto body = [&](auto masked) {
+      constexpr bool MASKED = decltype(masked)::value;
+      constexpr int kMm = 2 * KS;          // MFMAs of one block
+      constexpr int kSlots = 4 * kMm;      // MFMAs of the step
+      constexpr int kAhead = 4;
+      f32x16 sacc[2], dpacc[2];
+      i32x4 pb[2][2], dsb[2][2];   // packed P and dS operands (16 rows each)
+      // operand of slot t
+      auto read_op = [&](int t) -> bf16x8 {
+        const int blk = t / kMm, i = t % kMm;
+        if (blk < 2) {   // i = 2 ks + (0: Q row, 1: dO row)
+          const uint32_t off = (qrow ^ (uint32_t)((i >> 1) << 5)) + (uint32_t)(blk * 32 * HD * 2);
+          return lds_read8(reinterpret_cast<const bf16_t *>(lds_at((i & 1) ? tD : tQ, off)));
+        }
+        const int qb = blk - 2, u = (i >> 1) / DB, db = (i >> 1) % DB;   // i = 2 (u DB + db) + (0: dO^T, 1: Q^T)
+        return tro.operand((i & 1) ? tQ : tD, qb * 32 + 16 * u, db);
+      };
+      auto mma = [&](int t, const bf16x8 &op) {
+        const int blk = t / kMm, i = t % kMm;
+        if (blk < 2) {
+          if (i & 1) dpacc[blk] = mfma32(op, vf[i >> 1], dpacc[blk]);
+          else sacc[blk] = mfma32(op, kf[i >> 1], sacc[blk]);
+        } else {
+          const int qb = blk - 2, u = (i >> 1) / DB, db = (i >> 1) % DB;
+          if (i & 1) dkacc[db] = mfma32(op, __builtin_bit_cast(bf16x8, dsb[qb][u]), dkacc[db]);
+          else dvacc[db] = mfma32(op, __builtin_bit_cast(bf16x8, pb[qb][u]), dvacc[db]);
+        }
+      };
+      // scores 2 t, 2 t + 1 of row block qb: P (masked to 0) and dS, packed
+      // straight into the operand words (the accumulators are only read)
+      auto soft_pair = [&](int qb, int t) {
+        const int r0 = 2 * t;
+        const int ql = qb * 32 + 8 * (r0 >> 2) + 4 * hi + (r0 & 3);
+        const float2 l2 = *reinterpret_cast<const float2 *>(&tL[ql]);
+        const float2 e2 = *reinterpret_cast<const float2 *>(&tE[ql]);
+        float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[qb][r0], c, -l2.x));
+        float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[qb][r0 + 1], c, -l2.y));
+        if constexpr (MASKED) {
+          const int2 m2 = *reinterpret_cast<const int2 *>(&tM[ql]);
+          const int2 c2 = *reinterpret_cast<const int2 *>(&tC[ql]);
+          p0 = ((key <= m2.x) & (kw >= c2.x)) ? p0 : 0.f;
+          p1 = ((key <= m2.y) & (kw >= c2.y)) ? p1 : 0.f;
+        }
+        pb[qb][t >> 2][t & 3] = (int)cvt2(p0, p1);
+        dsb[qb][t >> 2][t & 3] = (int)cvt2(p0 * (dpacc[qb][r0] - e2.x), p1 * (dpacc[qb][r0 + 1] - e2.y));
+      };
 #pragma unroll
       for (int qb = 0; qb < 2; ++qb) {
-        f32x16 sacc = zero16(), dpacc = zero16();
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-          const int off = (qb * 32 + l32) * HD + (((2 * ks + hi) ^ qrow_sw) << 3);
-          sacc = mfma32(lds_read8(tQ + off), kf[ks], sacc);
-          dpacc = mfma32(lds_read8(tD + off), vf[ks], dpacc);
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int ql0 = qb * 32 + 8 * i + 4 * hi;
-          const f32x4 l4 = *reinterpret_cast<const f32x4 *>(&tL[ql0]);
-          const f32x4 e4 = *reinterpret_cast<const f32x4 *>(&tE[ql0]);
-          i32x4 m4 = {-1, -1, -1, -1}, v4 = {kWX, kWX, kWX, kWX};
-          if (partial) {
-            m4 = *reinterpret_cast<const i32x4 *>(&tM[ql0]);
-            v4 = *reinterpret_cast<const i32x4 *>(&tC[ql0]);
-          }
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int r = 4 * i + e;
-            float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[r], a.scale_log2, -l4[e]));
-            if (partial) {
-              const bool ok = (key <= m4[e]) & (kw >= v4[e]);
-              p = ok ? p : 0.f;
-            }
-            sacc[r] = p;
-            dpacc[r] = p * (dpacc[r] - e4[e]);
-          }
-        }
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const bf16x8 pb = pack8(sacc[8 * u + 0], sacc[8 * u + 1], sacc[8 * u + 2], sacc[8 * u + 3],
-                                  sacc[8 * u + 4], sacc[8 * u + 5], sacc[8 * u + 6], sacc[8 * u + 7]);
-          const bf16x8 dsb = pack8(dpacc[8 * u + 0], dpacc[8 * u + 1], dpacc[8 * u + 2], dpacc[8 * u + 3],
-                                   dpacc[8 * u + 4], dpacc[8 * u + 5], dpacc[8 * u + 6], dpacc[8 * u + 7]);
-#pragma unroll
-          for (int db = 0; db < DB; ++db) {
-            dvacc[db] = mfma32(lds_tr_operand<HD>(tD, tl, qb * 32 + 16 * u, db), pb, dvacc[db]);
-            dkacc[db] = mfma32(lds_tr_operand<HD>(tQ, tl, qb * 32 + 16 * u, db), dsb, dkacc[db]);
-          }
-        }
+        sacc[qb] = zero16();
+        dpacc[qb] = zero16();
       }
+      bf16x8 ring[kAhead];
+#pragma unroll
+      for (int t = 0; t < kAhead; ++t) ring[t] = read_op(t);
+#pragma unroll
+      for (int t = 0; t < kSlots; ++t) {
+        const bf16x8 op = ring[t % kAhead];
+        if (t + kAhead < kSlots) ring[t % kAhead] = read_op(t + kAhead);
+        mma(t, op);
+        // the softmax of a row block rides on the next block's MFMAs, one
+        // pair of scores every other slot (8 pairs per block)
+        const int blk = t / kMm, i = t % kMm;
+        if ((blk == 1 || blk == 2) && (i & 1) && (i >> 1) < 8) soft_pair(blk - 1, i >> 1);
+        if ((blk == 1 || blk == 2) && i == kMm - 1) {
+#pragma unroll
+          for (int pr = kMm / 2; pr < 8; ++pr) soft_pair(blk - 1, pr);   // HD = 64: the rest
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    };
+    if (q0 < a.S) {
+      if (partial) body(std::true_type{});
+      else body(std::false_type{});
     }
 
     if (j + 1 < nstep)
