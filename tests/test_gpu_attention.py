@@ -119,10 +119,14 @@ def test_transformers_wrapper_contract(mga, dev):
 @pytest.mark.parametrize("cfg", [
     dict(name="config2", n_reg=4096, n_anchor=256, draft=4, P=8192),
     dict(name="config5", n_reg=2048, n_anchor=512, draft=8, P=16384, every=4),
-])
+    # the last chunk of config 3's stream and of config 4's 32 full chunks
+    dict(name="config3_last", n_reg=4096, n_anchor=512, draft=4, P=28672),
+    dict(name="config4_last", n_reg=4096, n_anchor=256, draft=4, P=126976),
+], ids=lambda c: c["name"])
 def test_attention_full_config(mga, dev, cfg):
-    """Full Qwen3-8B attention geometry (32 q / 8 kv heads, D = 128) against an
-    fp32 dense reference on the GPU fed the same bf16 values."""
+    """Full attention geometry of Qwen3-8B / Llama-3.1-8B (32 q / 8 kv heads,
+    D = 128) against an fp32 dense reference on the GPU fed the same bf16
+    values, up to config 4's 131 072-token cache."""
     Hq, Hkv, D = 32, 8, 128
     seq, q, k, v, kp, vp, do, o, lse = run_case(
         mga, dev, cfg["n_reg"], cfg["n_anchor"], cfg["draft"], cfg["P"], Hq, Hkv, D, seed=2,
