@@ -147,6 +147,41 @@ int mga_attn_bwd(const void *q, int64_t q_sh, int64_t q_ss,
                  int32_t S, int32_t L, int32_t P, int32_t Hq, int32_t Hkv,
                  int32_t head_dim, int32_t dtype, float scale, int32_t passes, void *stream);
 
+/*
+ * Stable soft cross-entropy of the MTP sampler loss, row by row over n_rows
+ * rows of n_cols logits (row r of a [rows, cols] operand starts at
+ * base + r * row_stride elements; columns contiguous). For student logits x
+ * and teacher logits t (the same dtype code, MGA_DTYPE_BF16 or MGA_DTYPE_F32):
+ *   mx = max x, dx = max(sum e^{x - mx}, 1e-20), mt = max t,
+ *   dt = max(sum e^{t - mt}, 1e-20),
+ *   row_loss[r] = -(sum e^{t - mt} x) / dt + mx + log dx,
+ *   stats = [mx[n_rows], dx[n_rows], mt[n_rows], dt[n_rows]] (fp32).
+ * The caller sums row_loss (StableSoftCrossEntropy.forward returns that sum).
+ * workspace: mga_soft_ce_workspace_floats(n_rows, n_cols) fp32 values.
+ * Replaces stable_soft_ce_forward_kernel_{auto,manual}
+ * (mtp_glora/core/loss.py:63-179) as launched by
+ * StableSoftCrossEntropy.forward (loss.py:259-296).
+ */
+int64_t mga_soft_ce_workspace_floats(int32_t n_rows, int32_t n_cols);
+int mga_soft_ce_fwd(const void *student, int64_t student_row_stride,
+                    const void *teacher, int64_t teacher_row_stride,
+                    int32_t n_rows, int32_t n_cols, int32_t dtype,
+                    float *row_loss, float *stats, float *workspace, void *stream);
+
+/*
+ * Backward of mga_soft_ce_fwd for the student (the teacher gets none):
+ *   grad[r, j] = grad_output * (e^{x - mx} / dx - e^{t - mt} / dt)
+ * written in the student's dtype; grad_output: one fp32 value in device
+ * memory (the upstream gradient of the summed loss); stats from the forward.
+ * Replaces stable_soft_ce_backward_kernel_{auto,manual} (loss.py:182-256) and
+ * the dtype cast of StableSoftCrossEntropy.backward (loss.py:298-330).
+ */
+int mga_soft_ce_bwd(const void *student, int64_t student_row_stride,
+                    const void *teacher, int64_t teacher_row_stride,
+                    int32_t n_rows, int32_t n_cols, int32_t dtype,
+                    const float *grad_output, const float *stats,
+                    void *grad, int64_t grad_row_stride, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

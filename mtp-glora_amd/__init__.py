@@ -9,6 +9,8 @@ The package mirrors the reference's operator boundaries for this path:
 * ``mtp_attention_forward``     - the ``ALL_ATTENTION_FUNCTIONS`` entry
   (signature of [tf]integrations/flex_attention.py:262)
 * ``build_mtp_block_mask``      - the BlockMask of collator.py:290-363
+* ``StableSoftCrossEntropy``    - the sampler's soft cross-entropy,
+  mtp_glora/core/loss.py:259-330
 
 All arithmetic runs in libmtp_glora_amd.so (HIP, gfx950) through the C ABI in
 include/mtp_glora_amd.h. The directory name is not a Python identifier; import
@@ -18,11 +20,12 @@ from . import _lib, ops
 from .attention import mtp_attention, mtp_attention_forward, register
 from .block_mask import MTPBlockMask, build_mtp_block_mask
 from .cache import StreamingKVCache
+from .loss import StableSoftCrossEntropy
 from .manager import StreamingKVCacheManager
 
 __all__ = [
     "StreamingKVCache", "StreamingKVCacheManager", "MTPBlockMask", "build_mtp_block_mask",
-    "mtp_attention", "mtp_attention_forward", "register", "ops",
+    "mtp_attention", "mtp_attention_forward", "register", "ops", "StableSoftCrossEntropy",
 ]
 
 

@@ -206,4 +206,58 @@ int mga_attn_bwd(const void *q, int64_t q_sh, int64_t q_ss, const void *k, int64
   return check_launch("mga_attn_bwd");
 }
 
+int64_t mga_soft_ce_workspace_floats(int32_t n_rows, int32_t n_cols) {
+  if (n_rows <= 0 || n_cols <= 0) return 0;
+  return mga::soft_ce_workspace_floats(n_rows, n_cols);
+}
+
+namespace {
+
+// rows of a [n_rows, n_cols] operand; true in *vec when 16-byte vector loads apply
+int check_rows(const char *fn, const char *name, const void *p, int64_t rs, int32_t n_cols, int eb, bool *vec) {
+  if (!p) return fail(MGA_ERR_INVALID, "%s: %s is null", fn, name);
+  if (rs < n_cols) return fail(MGA_ERR_INVALID, "%s: %s row stride %lld < n_cols %d", fn, name, (long long)rs, n_cols);
+  *vec = *vec && aligned16(p) && ((rs * eb) & 15) == 0;
+  return MGA_OK;
+}
+
+int check_soft_ce(const char *fn, const void *x, int64_t xs, const void *t, int64_t ts, int32_t n_rows,
+                  int32_t n_cols, int32_t dtype, bool *vec) {
+  const int eb = elem_bytes(dtype);
+  if (!eb) return fail(MGA_ERR_INVALID, "%s: unknown dtype code %d", fn, dtype);
+  if (n_rows <= 0 || n_cols <= 0) return fail(MGA_ERR_INVALID, "%s: bad sizes (rows=%d cols=%d)", fn, n_rows, n_cols);
+  int rc = check_rows(fn, "student", x, xs, n_cols, eb, vec);
+  if (rc == MGA_OK) rc = check_rows(fn, "teacher", t, ts, n_cols, eb, vec);
+  return rc;
+}
+
+}  // namespace
+
+int mga_soft_ce_fwd(const void *student, int64_t student_row_stride, const void *teacher,
+                    int64_t teacher_row_stride, int32_t n_rows, int32_t n_cols, int32_t dtype, float *row_loss,
+                    float *stats, float *workspace, void *stream) {
+  bool vec = true;
+  int rc = check_soft_ce("mga_soft_ce_fwd", student, student_row_stride, teacher, teacher_row_stride, n_rows, n_cols,
+                         dtype, &vec);
+  if (rc != MGA_OK) return rc;
+  if (!row_loss || !stats || !workspace) return fail(MGA_ERR_INVALID, "mga_soft_ce_fwd: null output or workspace");
+  mga::launch_soft_ce_fwd(student, student_row_stride, teacher, teacher_row_stride, n_rows, n_cols,
+                          dtype == MGA_DTYPE_F32, vec, row_loss, stats, workspace, (hipStream_t)stream);
+  return check_launch("mga_soft_ce_fwd");
+}
+
+int mga_soft_ce_bwd(const void *student, int64_t student_row_stride, const void *teacher,
+                    int64_t teacher_row_stride, int32_t n_rows, int32_t n_cols, int32_t dtype,
+                    const float *grad_output, const float *stats, void *grad, int64_t grad_row_stride, void *stream) {
+  bool vec = true;
+  int rc = check_soft_ce("mga_soft_ce_bwd", student, student_row_stride, teacher, teacher_row_stride, n_rows, n_cols,
+                         dtype, &vec);
+  if (rc == MGA_OK) rc = check_rows("mga_soft_ce_bwd", "grad", grad, grad_row_stride, n_cols, elem_bytes(dtype), &vec);
+  if (rc != MGA_OK) return rc;
+  if (!grad_output || !stats) return fail(MGA_ERR_INVALID, "mga_soft_ce_bwd: null grad_output or stats");
+  mga::launch_soft_ce_bwd(student, student_row_stride, teacher, teacher_row_stride, n_rows, n_cols,
+                          dtype == MGA_DTYPE_F32, vec, grad_output, stats, grad, grad_row_stride, (hipStream_t)stream);
+  return check_launch("mga_soft_ce_bwd");
+}
+
 }  // extern "C"

@@ -290,6 +290,9 @@ struct TileList {
       const int e = cb + (threadIdx.x & 63);
       val = e < npart ? pidx[e] : (e < ntot ? fidx[e - npart] : 0);
       base = cb;
+      // wait for the refill here (once per 64 tiles): left to the use, the
+      // wait would sit on every call and drain all loads in flight
+      __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));   // vmcnt(0) only
     }
     return __builtin_amdgcn_readlane(val, it & 63);
   }

@@ -47,4 +47,13 @@ constexpr int kBwdDq = 1;
 constexpr int kBwdDkDv = 2;
 void launch_attn_bwd(const AttnArgs &a, int head_dim, bool is_f32, int passes, hipStream_t stream);
 
+// Stable soft cross-entropy (mga_soft_ce.hip). Rows of V columns; row strides
+// in elements; vec: 16-byte vector loads (every row start 16-byte aligned).
+int64_t soft_ce_workspace_floats(int32_t n_rows, int32_t n_cols);
+void launch_soft_ce_fwd(const void *x, int64_t xs, const void *t, int64_t ts, int32_t N, int32_t V, bool is_f32,
+                        bool vec, float *loss, float *stats, float *ws, hipStream_t stream);
+void launch_soft_ce_bwd(const void *x, int64_t xs, const void *t, int64_t ts, int32_t N, int32_t V, bool is_f32,
+                        bool vec, const float *grad_out, const float *stats, void *g, int64_t gs,
+                        hipStream_t stream);
+
 }  // namespace mga
