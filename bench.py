@@ -104,6 +104,54 @@ class EventTimer:
         return e0.elapsed_time(e1) / n
 
 
+QWEN3_VOCAB = 151936
+
+
+def soft_ce_phase(torch, mga, timer, rows: int, vocab: int, n: int, cpu_rows: int) -> dict:
+    """The sampler's soft cross-entropy (StableSoftCrossEntropy) at [1, rows,
+    vocab] bf16: forward and backward kernel time (HIP events), bytes moved
+    against the HBM peak, and the reference's math as torch eager on the CPU
+    for ``cpu_rows`` rows (the reference's kernel is Triton, GPU-only)."""
+    from importlib import import_module
+    lossmod = import_module("mtp-glora_amd.loss")
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(SEED + 7)
+    x = (torch.randn(1, rows, vocab, generator=g, device=dev) * 3).bfloat16()
+    t = (torch.randn(1, rows, vocab, generator=g, device=dev) * 3).bfloat16()
+    go = torch.ones((), device=dev)
+    loss, stats = lossmod.soft_ce_forward(x, t)
+    t_f = timer(lambda: lossmod.soft_ce_forward(x, t), n)
+    t_b = timer(lambda: lossmod.soft_ce_backward(x, t, stats, go), n)
+    elems = rows * vocab
+    fwd_bytes = 2 * elems * 2                 # student and teacher read once
+    bwd_bytes = 3 * elems * 2                 # both read, the bf16 gradient written
+    fwd_gbps = fwd_bytes / (t_f * 1e-3) / 1e9
+    bwd_gbps = bwd_bytes / (t_b * 1e-3) / 1e9
+    # CPU: the reference's formulas (loss.py:14-28 forward, autograd backward)
+    xc = x[0, :cpu_rows].float().cpu()
+    tc = t[0, :cpu_rows].float().cpu()
+    secs = []
+    for _ in range(4):
+        xr = xc.clone().requires_grad_()
+        t0 = time.perf_counter()
+        mx = xr.amax(dim=-1, keepdim=True)
+        dx = (xr - mx).exp().sum(dim=-1, keepdim=True).clamp_min(1e-20)
+        mt = tc.amax(dim=-1, keepdim=True)
+        dt = (tc - mt).exp().sum(dim=-1, keepdim=True).clamp_min(1e-20)
+        ce = (-(((tc - mt).exp() * xr).sum(dim=-1, keepdim=True) / dt) + mx + dx.log()).sum()
+        ce.backward()
+        secs.append(time.perf_counter() - t0)
+    cpu_s = sorted(secs[1:])[1]
+    return {"rows": rows, "vocab": vocab, "dtype": "bf16",
+            "fwd_ms": round(t_f, 4), "bwd_ms": round(t_b, 4),
+            "fwd_GBps": round(fwd_gbps, 1), "bwd_GBps": round(bwd_gbps, 1),
+            "fwd_frac": round(fwd_gbps / PEAK_HBM_GBPS, 4), "bwd_frac": round(bwd_gbps / PEAK_HBM_GBPS, 4),
+            "peak": PEAK_HBM_GBPS, "bytes": {"fwd": fwd_bytes, "bwd": bwd_bytes},
+            "cpu_rows_per_s": round(cpu_rows / cpu_s, 1), "gpu_rows_per_s": round(rows / ((t_f + t_b) * 1e-3), 1),
+            "cpu_sample": f"torch eager fp32 on the CPU, the reference's formulas, {cpu_rows} rows, fwd + bwd, "
+                          f"median of 3 after a warm-up, {torch.get_num_threads()} threads"}
+
+
 def graph_time(torch, fn, n: int, reps: int = 5) -> float:
     """Average duration of ``fn`` captured ``n`` times into one HIP graph
     (removes host launch gaps from microsecond kernels)."""
@@ -213,6 +261,11 @@ def pmc_pass(torch, mga, libc, q, k, v, do, kp, cache, chunk0, P, S, R, Hkv, D, 
     app_k = torch.empty(Hkv, R + 16, D, dtype=torch.bfloat16, device=dev)
     app_v = torch.empty_like(app_k)
     ops.kv_append(k.detach(), v.detach(), app_k, app_v, dst_offset=0, idx=idx, n_rows=R)
+    lossmod = importlib.import_module("mtp-glora_amd.loss")
+    xs = torch.randn(1, 256, QWEN3_VOCAB, device=dev).bfloat16()
+    ts = torch.randn(1, 256, QWEN3_VOCAB, device=dev).bfloat16()
+    _, st = lossmod.soft_ce_forward(xs, ts)
+    lossmod.soft_ce_backward(xs, ts, st, torch.ones((), device=dev))
     torch.cuda.synchronize()
     calib = Hkv * CALIB_ROWS * D * 2 * 2
     print(json.dumps({"pmc_pass": True, "calibration": {"kernel": "kv_copy_rows_kernel",
@@ -434,6 +487,7 @@ def main() -> int:
 
     phases = {"mask_build": t_mask, "fwd": t_fwd, "bwd_dq_pass": t_dq, "bwd_dkdv_pass": t_dkdv,
               "append_commit": t_commit, "append_stage": t_stage}
+    soft_ce = soft_ce_phase(torch, mga, timer, int(anchors.numel()), QWEN3_VOCAB, n, cpu_rows=16)
     traffic = load_traffic(args.traffic, args.config)
     credited = {"fwd": fl_fwd, "bwd_dq_pass": fl_dq, "bwd_dkdv_pass": fl_dkdv}
     dom = max(credited, key=lambda kname: phases[kname])
@@ -475,6 +529,7 @@ def main() -> int:
         "phases_ms": {kname: round(t, 5) for kname, t in phases.items()},
         "hbm_traffic_bytes": ({PHASE_KERNEL[k_]: traffic.get(PHASE_KERNEL[k_]) for k_ in PHASE_KERNEL}
                               if traffic else None),
+        "soft_ce": soft_ce,
         "host_ms_per_step": round(host_ms, 4),
     }
 
