@@ -152,6 +152,82 @@ def soft_ce_phase(torch, mga, timer, rows: int, vocab: int, n: int, cpu_rows: in
                           f"median of 3 after a warm-up, {torch.get_num_threads()} threads"}
 
 
+def qk_rope_phase(torch, timer, S: int, Hq: int, Hkv: int, D: int, n: int, cpu_tokens: int) -> dict:
+    """Qwen3 q_norm / k_norm + rotary embedding (qk_norm_rope) at the chunk's
+    [1, S, H, D] bf16 projections: forward and backward kernel time (HIP
+    events around a graph of 20 launches), bytes against the HBM peak; the
+    reference's ops
+    (Qwen3RMSNorm + apply_rotary_pos_emb, modeling_qwen3.py:274-279) as torch
+    eager on the same GPU for comparison, and on the CPU for ``cpu_tokens``."""
+    from importlib import import_module
+    rope = import_module("mtp-glora_amd.rope")
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(SEED + 9)
+    bf = torch.bfloat16
+    q = torch.randn(1, S, Hq, D, generator=g, device=dev).to(bf)
+    k = torch.randn(1, S, Hkv, D, generator=g, device=dev).to(bf)
+    qw = (1 + 0.1 * torch.randn(D, generator=g, device=dev)).to(bf)
+    kw = (1 + 0.1 * torch.randn(D, generator=g, device=dev)).to(bf)
+    pos = torch.arange(S, device=dev, dtype=torch.float32)[:, None]
+    inv = 1e6 ** (-torch.arange(0, D, 2, device=dev, dtype=torch.float32) / D)
+    emb = torch.cat([pos * inv, pos * inv], dim=-1)
+    cos, sin = emb.cos().to(bf)[None], emb.sin().to(bf)[None]
+    gq = torch.randn(1, S, Hq, D, generator=g, device=dev).to(bf)
+    gk = torch.randn(1, S, Hkv, D, generator=g, device=dev).to(bf)
+    _, _, rstd = rope.norm_rope_forward(q, k, qw, kw, cos, sin, 1e-6)
+    # one launch of tens of microseconds: time it inside a HIP graph, so the
+    # host's argument checks and allocations between launches are not counted
+    t_f = graph_time(torch, lambda: rope.norm_rope_forward(q, k, qw, kw, cos, sin, 1e-6), 20)
+    t_b = graph_time(torch, lambda: rope.norm_rope_backward(q, k, qw, kw, cos, sin, rstd, gq, gk), 20)
+    t_f_eager = timer(lambda: rope.norm_rope_forward(q, k, qw, kw, cos, sin, 1e-6), n)
+    rows = S * (Hq + Hkv)
+    table = 2 * S * D * 2                       # cos and sin rows
+    fwd_bytes = 2 * rows * D * 2 + rows * 4 + table
+    bwd_bytes = 3 * rows * D * 2 + rows * 4 + table
+    fwd_gbps = fwd_bytes / (t_f * 1e-3) / 1e9
+    bwd_gbps = bwd_bytes / (t_b * 1e-3) / 1e9
+
+    def reference_ops(qx, kx, c, s_, wq, wk):
+        def norm(x, w):
+            xf = x.float()
+            xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-6)
+            return w * xf.to(x.dtype)
+
+        def rot(x):
+            return torch.cat((-x[..., D // 2:], x[..., :D // 2]), dim=-1)
+        qn, kn = norm(qx, wq).transpose(1, 2), norm(kx, wk).transpose(1, 2)
+        c, s_ = c.unsqueeze(1), s_.unsqueeze(1)
+        return qn * c + rot(qn) * s_, kn * c + rot(kn) * s_
+
+    def eager_step(qx, kx, c, s_, wq, wk, go_q, go_k):
+        qx = qx.detach().requires_grad_()
+        kx = kx.detach().requires_grad_()
+        eq, ek = reference_ops(qx, kx, c, s_, wq, wk)
+        torch.autograd.backward([eq, ek], [go_q.transpose(1, 2), go_k.transpose(1, 2)])
+
+    t_eager = timer(lambda: eager_step(q, k, cos, sin, qw, kw, gq, gk), n)
+    args_cpu = [t_[:, :cpu_tokens].cpu() if t_.dim() == 4 else t_.cpu() for t_ in (q, k)]
+    c_cpu, s_cpu = cos[:, :cpu_tokens].cpu(), sin[:, :cpu_tokens].cpu()
+    secs = []
+    for _ in range(4):
+        t0 = time.perf_counter()
+        eager_step(args_cpu[0], args_cpu[1], c_cpu, s_cpu, qw.cpu(), kw.cpu(), gq[:, :cpu_tokens].cpu(),
+                   gk[:, :cpu_tokens].cpu())
+        secs.append(time.perf_counter() - t0)
+    cpu_s = sorted(secs[1:])[1]
+    return {"tokens": S, "Hq": Hq, "Hkv": Hkv, "head_dim": D, "dtype": "bf16",
+            "fwd_ms": round(t_f, 5), "bwd_ms": round(t_b, 5),
+            "fwd_GBps": round(fwd_gbps, 1), "bwd_GBps": round(bwd_gbps, 1),
+            "fwd_frac": round(fwd_gbps / PEAK_HBM_GBPS, 4), "bwd_frac": round(bwd_gbps / PEAK_HBM_GBPS, 4),
+            "peak": PEAK_HBM_GBPS, "bytes": {"fwd": fwd_bytes, "bwd": bwd_bytes},
+            "fwd_ms_eager_launches": round(t_f_eager, 5),
+            "torch_eager_gpu_fwd_bwd_ms": round(t_eager, 4),
+            "cpu_tokens_per_s": round(cpu_tokens / cpu_s, 1),
+            "gpu_tokens_per_s": round(S / ((t_f + t_b) * 1e-3), 1),
+            "cpu_sample": f"the reference's ops as torch eager bf16 on the CPU, fwd + bwd, {cpu_tokens} tokens, "
+                          f"median of 3 after a warm-up, {torch.get_num_threads()} threads"}
+
+
 def graph_time(torch, fn, n: int, reps: int = 5) -> float:
     """Average duration of ``fn`` captured ``n`` times into one HIP graph
     (removes host launch gaps from microsecond kernels)."""
@@ -266,6 +342,14 @@ def pmc_pass(torch, mga, libc, q, k, v, do, kp, cache, chunk0, P, S, R, Hkv, D, 
     ts = torch.randn(1, 256, QWEN3_VOCAB, device=dev).bfloat16()
     _, st = lossmod.soft_ce_forward(xs, ts)
     lossmod.soft_ce_backward(xs, ts, st, torch.ones((), device=dev))
+    rope = importlib.import_module("mtp-glora_amd.rope")
+    Hq = q.shape[1]
+    qr_ = torch.randn(1, S, Hq, D, device=dev).bfloat16()
+    kr_ = torch.randn(1, S, Hkv, D, device=dev).bfloat16()
+    wr_ = torch.ones(D, device=dev).bfloat16()
+    cr_ = torch.ones(1, S, D, device=dev).bfloat16()
+    _, _, rs_ = rope.norm_rope_forward(qr_, kr_, wr_, wr_, cr_, cr_, 1e-6)
+    rope.norm_rope_backward(qr_, kr_, wr_, wr_, cr_, cr_, rs_, qr_, kr_)
     torch.cuda.synchronize()
     calib = Hkv * CALIB_ROWS * D * 2 * 2
     print(json.dumps({"pmc_pass": True, "calibration": {"kernel": "kv_copy_rows_kernel",
@@ -488,6 +572,7 @@ def main() -> int:
     phases = {"mask_build": t_mask, "fwd": t_fwd, "bwd_dq_pass": t_dq, "bwd_dkdv_pass": t_dkdv,
               "append_commit": t_commit, "append_stage": t_stage}
     soft_ce = soft_ce_phase(torch, mga, timer, int(anchors.numel()), QWEN3_VOCAB, n, cpu_rows=16)
+    qk_rope = qk_rope_phase(torch, timer, S, Hq, Hkv, D, n, cpu_tokens=256)
     traffic = load_traffic(args.traffic, args.config)
     credited = {"fwd": fl_fwd, "bwd_dq_pass": fl_dq, "bwd_dkdv_pass": fl_dkdv}
     dom = max(credited, key=lambda kname: phases[kname])
@@ -530,6 +615,7 @@ def main() -> int:
         "hbm_traffic_bytes": ({PHASE_KERNEL[k_]: traffic.get(PHASE_KERNEL[k_]) for k_ in PHASE_KERNEL}
                               if traffic else None),
         "soft_ce": soft_ce,
+        "qk_norm_rope": qk_rope,
         "host_ms_per_step": round(host_ms, 4),
     }
 

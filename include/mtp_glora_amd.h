@@ -148,6 +148,49 @@ int mga_attn_bwd(const void *q, int64_t q_sh, int64_t q_ss,
                  int32_t head_dim, int32_t dtype, float scale, int32_t passes, void *stream);
 
 /*
+ * Qwen3 query / key normalisation and rotary embedding, fused:
+ *   for every token s and head h of q [S, Hq, D] (weight q_weight) and of
+ *   k [S, Hkv, D] (weight k_weight), with x = the row in fp32:
+ *     r = 1 / sqrt(mean(x * x) + eps),  n = T(w * T(x * r)),
+ *     out = T(T(n * cos[s]) + T(rotate_half(n) * sin[s])),
+ *     rotate_half(n) = [-n[D/2:], n[:D/2]],
+ *   T = rounding to the model dtype after each op, as the reference's torch ops
+ *   do; rstd[s * (Hq + Hkv) + row] = r (rows: the Hq query heads, then the Hkv
+ *   key heads) is saved for the backward.
+ * Operands are addressed base + s * token_stride + h * head_stride + d
+ * (elements); cos / sin are [S, D] with token stride cs_stride; D even, <= 128.
+ * Replaces q_norm / k_norm (Qwen3RMSNorm.forward,
+ * mtp_glora/models/modeling_qwen3.py:61-67) and apply_rotary_pos_emb
+ * (:118-149) as called by Qwen3Attention.forward (:274-279).
+ */
+int mga_qk_norm_rope_fwd(const void *q, int64_t q_token_stride, int64_t q_head_stride,
+                         const void *k, int64_t k_token_stride, int64_t k_head_stride,
+                         const void *q_weight, const void *k_weight,
+                         const void *cos, const void *sin, int64_t cs_stride,
+                         float eps, int32_t S, int32_t Hq, int32_t Hkv, int32_t head_dim, int32_t dtype,
+                         void *q_out, int64_t qo_token_stride, int64_t qo_head_stride,
+                         void *k_out, int64_t ko_token_stride, int64_t ko_head_stride,
+                         float *rstd, void *stream);
+
+/*
+ * Backward of mga_qk_norm_rope_fwd for q and k (the norm weights, cos and sin
+ * get no gradient): given the output gradients dq_out / dk_out, writes
+ *   dx = r * dy - (r^3 / D) * x * sum(dy * x),  dy = w * dn,
+ *   dn = g * cos + [g[D/2:] * sin[D/2:], -g[:D/2] * sin[:D/2]]
+ * (fp32, the forward's roundings taken as identity).
+ * Replaces the autograd backward of the ops above.
+ */
+int mga_qk_norm_rope_bwd(const void *q, int64_t q_token_stride, int64_t q_head_stride,
+                         const void *k, int64_t k_token_stride, int64_t k_head_stride,
+                         const void *q_weight, const void *k_weight,
+                         const void *cos, const void *sin, int64_t cs_stride, const float *rstd,
+                         int32_t S, int32_t Hq, int32_t Hkv, int32_t head_dim, int32_t dtype,
+                         const void *dq_out, int64_t dqo_token_stride, int64_t dqo_head_stride,
+                         const void *dk_out, int64_t dko_token_stride, int64_t dko_head_stride,
+                         void *dq, int64_t dq_token_stride, int64_t dq_head_stride,
+                         void *dk, int64_t dk_token_stride, int64_t dk_head_stride, void *stream);
+
+/*
  * Stable soft cross-entropy of the MTP sampler loss, row by row over n_rows
  * rows of n_cols logits (row r of a [rows, cols] operand starts at
  * base + r * row_stride elements; columns contiguous). For student logits x

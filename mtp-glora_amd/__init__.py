@@ -11,6 +11,9 @@ The package mirrors the reference's operator boundaries for this path:
 * ``build_mtp_block_mask``      - the BlockMask of collator.py:290-363
 * ``StableSoftCrossEntropy``    - the sampler's soft cross-entropy,
   mtp_glora/core/loss.py:259-330
+* ``qk_norm_rope`` / ``qwen3_attention_forward`` - q_norm, k_norm and
+  apply_rotary_pos_emb of Qwen3Attention.forward
+  (mtp_glora/models/modeling_qwen3.py:254-305), fused
 
 All arithmetic runs in libmtp_glora_amd.so (HIP, gfx950) through the C ABI in
 include/mtp_glora_amd.h. The directory name is not a Python identifier; import
@@ -22,10 +25,12 @@ from .block_mask import MTPBlockMask, build_mtp_block_mask
 from .cache import StreamingKVCache
 from .loss import StableSoftCrossEntropy
 from .manager import StreamingKVCacheManager
+from .rope import qk_norm_rope, qwen3_attention_forward
 
 __all__ = [
     "StreamingKVCache", "StreamingKVCacheManager", "MTPBlockMask", "build_mtp_block_mask",
     "mtp_attention", "mtp_attention_forward", "register", "ops", "StableSoftCrossEntropy",
+    "qk_norm_rope", "qwen3_attention_forward",
 ]
 
 

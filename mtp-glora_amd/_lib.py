@@ -40,6 +40,11 @@ SIGNATURES = {
                      _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64,
                      _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                      _I32, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _I32, _P],
+    "mga_qk_norm_rope_fwd": [_P, _I64, _I64, _P, _I64, _I64, _P, _P, _P, _P, _I64, _F32,
+                             _I32, _I32, _I32, _I32, _I32, _P, _I64, _I64, _P, _I64, _I64, _P, _P],
+    "mga_qk_norm_rope_bwd": [_P, _I64, _I64, _P, _I64, _I64, _P, _P, _P, _P, _I64, _P,
+                             _I32, _I32, _I32, _I32, _I32, _P, _I64, _I64, _P, _I64, _I64,
+                             _P, _I64, _I64, _P, _I64, _I64, _P],
     "mga_soft_ce_workspace_floats": [_I32, _I32],
     "mga_soft_ce_fwd": [_P, _I64, _P, _I64, _I32, _I32, _I32, _P, _P, _P, _P],
     "mga_soft_ce_bwd": [_P, _I64, _P, _I64, _I32, _I32, _I32, _P, _P, _P, _I64, _P],

@@ -206,6 +206,60 @@ int mga_attn_bwd(const void *q, int64_t q_sh, int64_t q_ss, const void *k, int64
   return check_launch("mga_attn_bwd");
 }
 
+namespace {
+
+int check_qk_rope(const char *fn, const void *q, const void *k, const void *qw, const void *kw, const void *c,
+                  const void *sn, const float *rstd, int32_t S, int32_t Hq, int32_t Hkv, int32_t D, int32_t dtype) {
+  if (!elem_bytes(dtype)) return fail(MGA_ERR_INVALID, "%s: unknown dtype code %d", fn, dtype);
+  if (S <= 0 || Hq <= 0 || Hkv <= 0) return fail(MGA_ERR_INVALID, "%s: bad sizes (S=%d Hq=%d Hkv=%d)", fn, S, Hq, Hkv);
+  if (D <= 0 || D > 128 || (D & 1)) return fail(MGA_ERR_INVALID, "%s: head_dim must be even and <= 128 (got %d)", fn, D);
+  if (!q || !k || !qw || !kw || !c || !sn || !rstd) return fail(MGA_ERR_INVALID, "%s: null pointer argument", fn);
+  return MGA_OK;
+}
+
+}  // namespace
+
+int mga_qk_norm_rope_fwd(const void *q, int64_t q_ss, int64_t q_hs, const void *k, int64_t k_ss, int64_t k_hs,
+                         const void *q_weight, const void *k_weight, const void *cos, const void *sin,
+                         int64_t cs_ss, float eps, int32_t S, int32_t Hq, int32_t Hkv, int32_t head_dim,
+                         int32_t dtype, void *q_out, int64_t qo_ss, int64_t qo_hs, void *k_out, int64_t ko_ss,
+                         int64_t ko_hs, float *rstd, void *stream) {
+  int rc = check_qk_rope("mga_qk_norm_rope_fwd", q, k, q_weight, k_weight, cos, sin, rstd, S, Hq, Hkv, head_dim, dtype);
+  if (rc != MGA_OK) return rc;
+  if (!q_out || !k_out) return fail(MGA_ERR_INVALID, "mga_qk_norm_rope_fwd: null output");
+  mga::QkRopeArgs a = {};
+  a.q = q; a.q_ss = q_ss; a.q_hs = q_hs;
+  a.k = k; a.k_ss = k_ss; a.k_hs = k_hs;
+  a.qw = q_weight; a.kw = k_weight; a.cos = cos; a.sin = sin; a.cs_ss = cs_ss;
+  a.qo = q_out; a.qo_ss = qo_ss; a.qo_hs = qo_hs;
+  a.ko = k_out; a.ko_ss = ko_ss; a.ko_hs = ko_hs;
+  a.rstd = rstd; a.eps = eps; a.S = S; a.Hq = Hq; a.Hkv = Hkv; a.D = head_dim;
+  mga::launch_qk_norm_rope(a, dtype == MGA_DTYPE_F32, false, (hipStream_t)stream);
+  return check_launch("mga_qk_norm_rope_fwd");
+}
+
+int mga_qk_norm_rope_bwd(const void *q, int64_t q_ss, int64_t q_hs, const void *k, int64_t k_ss, int64_t k_hs,
+                         const void *q_weight, const void *k_weight, const void *cos, const void *sin,
+                         int64_t cs_ss, const float *rstd, int32_t S, int32_t Hq, int32_t Hkv, int32_t head_dim,
+                         int32_t dtype, const void *dq_out, int64_t dqo_ss, int64_t dqo_hs, const void *dk_out,
+                         int64_t dko_ss, int64_t dko_hs, void *dq, int64_t dq_ss, int64_t dq_hs, void *dk,
+                         int64_t dk_ss, int64_t dk_hs, void *stream) {
+  int rc = check_qk_rope("mga_qk_norm_rope_bwd", q, k, q_weight, k_weight, cos, sin, rstd, S, Hq, Hkv, head_dim, dtype);
+  if (rc != MGA_OK) return rc;
+  if (!dq_out || !dk_out || !dq || !dk) return fail(MGA_ERR_INVALID, "mga_qk_norm_rope_bwd: null gradient pointer");
+  mga::QkRopeArgs a = {};
+  a.q = q; a.q_ss = q_ss; a.q_hs = q_hs;
+  a.k = k; a.k_ss = k_ss; a.k_hs = k_hs;
+  a.qw = q_weight; a.kw = k_weight; a.cos = cos; a.sin = sin; a.cs_ss = cs_ss;
+  a.dqo = dq_out; a.dqo_ss = dqo_ss; a.dqo_hs = dqo_hs;
+  a.dko = dk_out; a.dko_ss = dko_ss; a.dko_hs = dko_hs;
+  a.dq = dq; a.dq_ss = dq_ss; a.dq_hs = dq_hs;
+  a.dk = dk; a.dk_ss = dk_ss; a.dk_hs = dk_hs;
+  a.rstd = const_cast<float *>(rstd); a.S = S; a.Hq = Hq; a.Hkv = Hkv; a.D = head_dim;
+  mga::launch_qk_norm_rope(a, dtype == MGA_DTYPE_F32, true, (hipStream_t)stream);
+  return check_launch("mga_qk_norm_rope_bwd");
+}
+
 int64_t mga_soft_ce_workspace_floats(int32_t n_rows, int32_t n_cols) {
   if (n_rows <= 0 || n_cols <= 0) return 0;
   return mga::soft_ce_workspace_floats(n_rows, n_cols);

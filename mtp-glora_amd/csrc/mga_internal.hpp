@@ -47,6 +47,25 @@ constexpr int kBwdDq = 1;
 constexpr int kBwdDkDv = 2;
 void launch_attn_bwd(const AttnArgs &a, int head_dim, bool is_f32, int passes, hipStream_t stream);
 
+// Fused Qwen3 q/k RMSNorm + rotary embedding (mga_qk_rope.hip). Operands are
+// [S, heads, D] addressed with (token stride, head stride) in elements; cos
+// and sin [S, D] with token stride cs_ss; rstd [S, Hq + Hkv] (token-major).
+struct QkRopeArgs {
+  const void *q; int64_t q_ss, q_hs;
+  const void *k; int64_t k_ss, k_hs;
+  const void *qw, *kw, *cos, *sin; int64_t cs_ss;
+  void *qo; int64_t qo_ss, qo_hs;     // forward outputs
+  void *ko; int64_t ko_ss, ko_hs;
+  const void *dqo; int64_t dqo_ss, dqo_hs;   // backward: gradients of the outputs
+  const void *dko; int64_t dko_ss, dko_hs;
+  void *dq; int64_t dq_ss, dq_hs;     // backward outputs
+  void *dk; int64_t dk_ss, dk_hs;
+  float *rstd;
+  float eps;
+  int32_t S, Hq, Hkv, D;
+};
+void launch_qk_norm_rope(const QkRopeArgs &a, bool is_f32, bool backward, hipStream_t stream);
+
 // Stable soft cross-entropy (mga_soft_ce.hip). Rows of V columns; row strides
 // in elements; vec: 16-byte vector loads (every row start 16-byte aligned).
 int64_t soft_ce_workspace_floats(int32_t n_rows, int32_t n_cols);

@@ -183,12 +183,16 @@ def _check(name, got, ref, max_abs, mean_abs):
     assert err.max().item() <= max_abs and err.mean().item() <= mean_abs, name
 
 
-def test_config1_chunk_stream_through_transformers_qwen3(dev):
+def _stream_against_reference(dev, fused_qk_norm_rope: bool, monkeypatch):
     mga = importlib.import_module("mtp-glora_amd")
     mga.register("mtp_hip")
     AttentionInterface.register("mtp_dense_ref", dense_masked_attention)
     chunks = make_sequence(0)
-    hip_logits, hip_grads = run_hip(mga, chunks, dev)
+    with monkeypatch.context() as m:
+        if fused_qk_norm_rope:
+            from transformers.models.qwen3 import modeling_qwen3
+            m.setattr(modeling_qwen3.Qwen3Attention, "forward", mga.qwen3_attention_forward)
+        hip_logits, hip_grads = run_hip(mga, chunks, dev)
     ref_logits, ref_grads = run_reference(chunks)
     one_pass = run_single_pass(chunks)
     for c in range(len(chunks)):
@@ -199,3 +203,14 @@ def test_config1_chunk_stream_through_transformers_qwen3(dev):
         scale = r.abs().max().item()
         assert scale > 0
         _check(f"lora grad {i} (scale {scale:.2e})", g / scale, r / scale, 2e-2, 2e-3)
+
+
+def test_config1_chunk_stream_through_transformers_qwen3(dev, monkeypatch):
+    _stream_against_reference(dev, False, monkeypatch)
+
+
+def test_config1_chunk_stream_with_fused_qk_norm_rope(dev, monkeypatch):
+    """The same stream with Qwen3Attention.forward replaced by the adapter that
+    runs q_norm / k_norm / rope as one HIP kernel (forward and backward): the
+    LoRA gradients of q_proj and k_proj flow through its backward."""
+    _stream_against_reference(dev, True, monkeypatch)
