@@ -349,7 +349,8 @@ def pmc_pass(torch, mga, libc, q, k, v, do, kp, cache, chunk0, P, S, R, Hkv, D, 
     wr_ = torch.ones(D, device=dev).bfloat16()
     cr_ = torch.ones(1, S, D, device=dev).bfloat16()
     _, _, rs_ = rope.norm_rope_forward(qr_, kr_, wr_, wr_, cr_, cr_, 1e-6)
-    rope.norm_rope_backward(qr_, kr_, wr_, wr_, cr_, cr_, rs_, qr_, kr_)
+    gq_, gk_ = torch.randn_like(qr_), torch.randn_like(kr_)   # gradients: their own memory
+    rope.norm_rope_backward(qr_, kr_, wr_, wr_, cr_, cr_, rs_, gq_, gk_)
     torch.cuda.synchronize()
     calib = Hkv * CALIB_ROWS * D * 2 * 2
     print(json.dumps({"pmc_pass": True, "calibration": {"kernel": "kv_copy_rows_kernel",
