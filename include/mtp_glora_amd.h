@@ -191,6 +191,47 @@ int mga_qk_norm_rope_bwd(const void *q, int64_t q_token_stride, int64_t q_head_s
                          void *dk, int64_t dk_token_stride, int64_t dk_head_stride, void *stream);
 
 /*
+ * Gated LoRA linear layer, bf16 (GatedLoRALinear.forward,
+ * mtp_glora/models/layers/gated_lora.py:51-53):
+ *   y = x W^T + scaling * B(A(dropout(x))) * gate
+ * for x [S, K] (row stride x_rs), W [N, K], A = lora_A.weight [rank, K],
+ * B = lora_B.weight [N, rank], gate [S] fp32 (NULL = 1; the reference's
+ * clamped gate mask). Writes y [S, N] and, for the backward, t [S, rpad]
+ * (rpad = rank rounded up to 32; t = T(T(scaling * T(h A^T)) * gate), T =
+ * bf16 rounding, h = dropout(x)) and, when dropout_p > 0, h [S, K].
+ * Dropout keeps element i of the flattened [S, K] input by a hash of
+ * (seed, i) with probability 1 - round(65536 p) / 65536 and scales kept
+ * elements by 1 / (1 - p). K must be a multiple of 16; x, lora_A and h are read
+ * or written with 16-byte vectors (aligned rows, strides multiples of 8).
+ * workspace: mga_gated_lora_workspace_bytes(S, K, N, rank) bytes.
+ * The plain GEMMs run in hipBLASLt on the same stream.
+ */
+int64_t mga_gated_lora_workspace_bytes(int32_t S, int32_t K, int32_t N, int32_t rank);
+int mga_gated_lora_fwd(const void *x, int64_t x_rs, const void *weight, int64_t w_rs,
+                       const void *lora_a, int64_t a_rs, const void *lora_b, int64_t b_rs,
+                       const float *gate, float scaling, double dropout_p, uint64_t seed,
+                       int32_t S, int32_t K, int32_t N, int32_t rank,
+                       void *y, int64_t y_rs, void *t, int64_t t_rs, void *h, int64_t h_rs,
+                       void *workspace, int64_t workspace_bytes, void *stream);
+
+/*
+ * Backward of mga_gated_lora_fwd (the autograd backward of the reference's
+ * GatedLoRALinear.forward with the base weight frozen, gated_lora.py:51-53,
+ * :56-58): from grad_y [S, N] and the forward's x, h, t and seed,
+ *   grad_B = grad_y^T t,  d_a = T(T((grad_y B) * gate) * scaling),
+ *   grad_x = T(grad_y W + T(mask * T(d_a A) / (1 - p))),  grad_A = d_a^T h.
+ * grad_x, grad_a, grad_b may be NULL to skip them.
+ */
+int mga_gated_lora_bwd(const void *grad_y, int64_t gy_rs, const void *x, int64_t x_rs,
+                       const void *h, int64_t h_rs, const void *weight, int64_t w_rs,
+                       const void *lora_a, int64_t a_rs, const void *lora_b, int64_t b_rs,
+                       const void *t, int64_t t_rs, const float *gate, float scaling,
+                       double dropout_p, uint64_t seed, int32_t S, int32_t K, int32_t N, int32_t rank,
+                       void *grad_x, int64_t gx_rs, void *grad_a, int64_t ga_rs,
+                       void *grad_b, int64_t gb_rs, void *workspace, int64_t workspace_bytes,
+                       void *stream);
+
+/*
  * Stable soft cross-entropy of the MTP sampler loss, row by row over n_rows
  * rows of n_cols logits (row r of a [rows, cols] operand starts at
  * base + r * row_stride elements; columns contiguous). For student logits x

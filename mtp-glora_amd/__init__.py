@@ -11,6 +11,8 @@ The package mirrors the reference's operator boundaries for this path:
 * ``build_mtp_block_mask``      - the BlockMask of collator.py:290-363
 * ``StableSoftCrossEntropy``    - the sampler's soft cross-entropy,
   mtp_glora/core/loss.py:259-330
+* ``GatedLoRALinear`` / ``apply_lora_to_model`` - the gated LoRA layers,
+  mtp_glora/models/layers/gated_lora.py
 * ``qk_norm_rope`` / ``qwen3_attention_forward`` - q_norm, k_norm and
   apply_rotary_pos_emb of Qwen3Attention.forward
   (mtp_glora/models/modeling_qwen3.py:254-305), fused
@@ -23,6 +25,7 @@ from . import _lib, ops
 from .attention import mtp_attention, mtp_attention_forward, register
 from .block_mask import MTPBlockMask, build_mtp_block_mask
 from .cache import StreamingKVCache
+from .lora import GatedLoRALinear, apply_lora_to_model, gated_lora_linear
 from .loss import StableSoftCrossEntropy
 from .manager import StreamingKVCacheManager
 from .rope import qk_norm_rope, qwen3_attention_forward
@@ -30,7 +33,7 @@ from .rope import qk_norm_rope, qwen3_attention_forward
 __all__ = [
     "StreamingKVCache", "StreamingKVCacheManager", "MTPBlockMask", "build_mtp_block_mask",
     "mtp_attention", "mtp_attention_forward", "register", "ops", "StableSoftCrossEntropy",
-    "qk_norm_rope", "qwen3_attention_forward",
+    "qk_norm_rope", "qwen3_attention_forward", "GatedLoRALinear", "apply_lora_to_model", "gated_lora_linear",
 ]
 
 

@@ -26,6 +26,8 @@ _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
 _I32 = ctypes.c_int32
 _F32 = ctypes.c_float
+_F64 = ctypes.c_double
+_U64 = ctypes.c_uint64
 SIGNATURES = {
     "mga_version": [],
     "mga_last_error": [],
@@ -45,11 +47,17 @@ SIGNATURES = {
     "mga_qk_norm_rope_bwd": [_P, _I64, _I64, _P, _I64, _I64, _P, _P, _P, _P, _I64, _P,
                              _I32, _I32, _I32, _I32, _I32, _P, _I64, _I64, _P, _I64, _I64,
                              _P, _I64, _I64, _P, _I64, _I64, _P],
+    "mga_gated_lora_workspace_bytes": [_I32, _I32, _I32, _I32],
+    "mga_gated_lora_fwd": [_P, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _F32, _F64, _U64,
+                           _I32, _I32, _I32, _I32, _P, _I64, _P, _I64, _P, _I64, _P, _I64, _P],
+    "mga_gated_lora_bwd": [_P, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _F32,
+                           _F64, _U64, _I32, _I32, _I32, _I32, _P, _I64, _P, _I64, _P, _I64, _P, _I64, _P],
     "mga_soft_ce_workspace_floats": [_I32, _I32],
     "mga_soft_ce_fwd": [_P, _I64, _P, _I64, _I32, _I32, _I32, _P, _P, _P, _P],
     "mga_soft_ce_bwd": [_P, _I64, _P, _I64, _I32, _I32, _I32, _P, _P, _P, _I64, _P],
 }
-_RESTYPES = {"mga_last_error": ctypes.c_char_p, "mga_soft_ce_workspace_floats": ctypes.c_int64}
+_RESTYPES = {"mga_last_error": ctypes.c_char_p, "mga_soft_ce_workspace_floats": ctypes.c_int64,
+             "mga_gated_lora_workspace_bytes": ctypes.c_int64}
 
 
 class MGAError(RuntimeError):

@@ -59,7 +59,8 @@ def build_library(verbose: bool = False, jobs: int = 4) -> Path:
         objs = list(ex.map(compile_one, sources))
     out = lib_path()
     tmp = out.with_suffix(".so.tmp")
-    cmd = [cc, "-shared", f"--offload-arch={ARCH}", "-fPIC", *map(str, objs), "-o", str(tmp)]
+    cmd = [cc, "-shared", f"--offload-arch={ARCH}", "-fPIC", *map(str, objs), "-o", str(tmp),
+           "-L/opt/rocm/lib", "-lhipblaslt"]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr}")

@@ -1,5 +1,6 @@
 // C ABI entry points (declared in include/mtp_glora_amd.h): argument checks,
 // then kernel launches on the caller's stream. No device allocation happens here.
+#include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
 
@@ -258,6 +259,169 @@ int mga_qk_norm_rope_bwd(const void *q, int64_t q_ss, int64_t q_hs, const void *
   a.rstd = const_cast<float *>(rstd); a.S = S; a.Hq = Hq; a.Hkv = Hkv; a.D = head_dim;
   mga::launch_qk_norm_rope(a, dtype == MGA_DTYPE_F32, true, (hipStream_t)stream);
   return check_launch("mga_qk_norm_rope_bwd");
+}
+
+namespace {
+
+constexpr int64_t kBlasWorkspace = int64_t(32) << 20;   // hipBLASLt workspace per call
+
+int64_t align256(int64_t b) { return (b + 255) & ~int64_t(255); }
+int64_t lora_rpad(int32_t rank) { return (rank + 31) / 32 * 32; }
+
+struct LoraWs {
+  void *blas, *u, *da, *at;
+};
+
+// [hipBLASLt workspace | u = dY B : S x rpad | d_a : S x rpad | A^T : K x rpad], bf16
+int64_t lora_ws_bytes(int32_t S, int32_t K, int32_t rank) {
+  const int64_t rp = lora_rpad(rank);
+  return kBlasWorkspace + 2 * align256((int64_t)S * rp * 2) + align256((int64_t)K * rp * 2);
+}
+
+LoraWs lora_ws(void *ws, int32_t S, int32_t rank) {
+  const int64_t rp = lora_rpad(rank);
+  char *p = static_cast<char *>(ws);
+  LoraWs w;
+  w.blas = p;
+  w.u = p + kBlasWorkspace;
+  w.da = static_cast<char *>(w.u) + align256((int64_t)S * rp * 2);
+  w.at = static_cast<char *>(w.da) + align256((int64_t)S * rp * 2);
+  return w;
+}
+
+int check_lora_sizes(const char *fn, int32_t S, int32_t K, int32_t N, int32_t rank, double p) {
+  if (S <= 0 || N <= 0 || K <= 0) return fail(MGA_ERR_INVALID, "%s: bad sizes (S=%d K=%d N=%d)", fn, S, K, N);
+  if (K % 16) return fail(MGA_ERR_INVALID, "%s: in_features must be a multiple of 16 (got %d)", fn, K);
+  if (rank < 1) return fail(MGA_ERR_INVALID, "%s: rank must be positive (got %d)", fn, rank);
+  if (!(p >= 0.0 && p < 1.0)) return fail(MGA_ERR_INVALID, "%s: dropout probability %g not in [0, 1)", fn, p);
+  return MGA_OK;
+}
+
+// A bf16 matrix read with 16-byte vectors along its rows.
+int check_vec_rows(const char *fn, const char *name, const void *ptr, int64_t rs, int64_t cols) {
+  if (!ptr) return fail(MGA_ERR_INVALID, "%s: %s is null", fn, name);
+  if (!aligned16(ptr)) return fail(MGA_ERR_INVALID, "%s: %s is not 16-byte aligned", fn, name);
+  if (rs < cols || rs % 8) return fail(MGA_ERR_INVALID, "%s: %s row stride %lld must be >= %lld and a multiple of 8",
+                                       fn, name, (long long)rs, (long long)cols);
+  return MGA_OK;
+}
+
+int check_rows_ld(const char *fn, const char *name, const void *ptr, int64_t rs, int64_t cols) {
+  if (!ptr) return fail(MGA_ERR_INVALID, "%s: %s is null", fn, name);
+  if (rs < cols) return fail(MGA_ERR_INVALID, "%s: %s row stride %lld < %lld", fn, name, (long long)rs,
+                             (long long)cols);
+  return MGA_OK;
+}
+
+uint32_t drop_threshold(double p) { return (uint32_t)llround(p * 65536.0); }
+float keep_scale(double p) { return (float)(1.0 / (1.0 - p)); }
+
+int blas(const char *fn, bool ta, bool tb, int64_t M, int64_t N, int64_t K, const void *A, int64_t lda, const void *B,
+         int64_t ldb, bool acc, void *D, int64_t ldd, const LoraWs &w, hipStream_t st) {
+  const char *err = nullptr;
+  if (mga::gemm_bf16(ta, tb, M, N, K, A, lda, B, ldb, acc, D, ldd, w.blas, (size_t)kBlasWorkspace, st, &err))
+    return fail(MGA_ERR_HIP, "%s: hipBLASLt GEMM (%lld x %lld x %lld): %s", fn, (long long)M, (long long)N,
+                (long long)K, err ? err : "error");
+  return MGA_OK;
+}
+
+}  // namespace
+
+int64_t mga_gated_lora_workspace_bytes(int32_t S, int32_t K, int32_t N, int32_t rank) {
+  (void)N;
+  if (S <= 0 || K <= 0 || rank <= 0) return 0;
+  return lora_ws_bytes(S, K, rank);
+}
+
+int mga_gated_lora_fwd(const void *x, int64_t x_rs, const void *weight, int64_t w_rs, const void *lora_a,
+                       int64_t a_rs, const void *lora_b, int64_t b_rs, const float *gate, float scaling,
+                       double dropout_p, uint64_t seed, int32_t S, int32_t K, int32_t N, int32_t rank, void *y,
+                       int64_t y_rs, void *t, int64_t t_rs, void *h, int64_t h_rs, void *workspace,
+                       int64_t workspace_bytes, void *stream) {
+  const char *fn = "mga_gated_lora_fwd";
+  int rc;
+  if ((rc = check_lora_sizes(fn, S, K, N, rank, dropout_p)) != MGA_OK) return rc;
+  const uint32_t thr = drop_threshold(dropout_p);
+  const int64_t rp = lora_rpad(rank);
+  if ((rc = check_vec_rows(fn, "x", x, x_rs, K)) != MGA_OK || (rc = check_rows_ld(fn, "weight", weight, w_rs, K)) ||
+      (rc = check_vec_rows(fn, "lora_A", lora_a, a_rs, K)) || (rc = check_rows_ld(fn, "lora_B", lora_b, b_rs, rank)) ||
+      (rc = check_rows_ld(fn, "output", y, y_rs, N)) || (rc = check_rows_ld(fn, "t", t, t_rs, rp)))
+    return rc;
+  if (thr > 0 && (rc = check_vec_rows(fn, "dropout output h", h, h_rs, K)) != MGA_OK) return rc;
+  if (!workspace || workspace_bytes < lora_ws_bytes(S, K, rank))
+    return fail(MGA_ERR_INVALID, "%s: workspace of %lld bytes needed", fn, (long long)lora_ws_bytes(S, K, rank));
+  const LoraWs w = lora_ws(workspace, S, rank);
+  hipStream_t st = (hipStream_t)stream;
+  // y = x W^T
+  if ((rc = blas(fn, false, true, S, N, K, x, x_rs, weight, w_rs, false, y, y_rs, w, st)) != MGA_OK) return rc;
+  // t = T(T(s T(dropout(x) A^T)) gate)
+  mga::LoraDownArgs a = {};
+  a.x = x; a.x_rs = x_rs; a.A = lora_a; a.a_rs = a_rs; a.gate = gate; a.scaling = scaling;
+  a.keep_scale = keep_scale(dropout_p); a.thr = thr; a.seed = seed; a.h = thr ? h : nullptr; a.h_rs = h_rs;
+  a.t = t; a.t_rs = t_rs; a.S = S; a.K = K; a.rank = rank;
+  mga::launch_lora_down(a, st);
+  if ((rc = check_launch(fn)) != MGA_OK) return rc;
+  // y += t B^T
+  if ((rc = blas(fn, false, true, S, N, rank, t, t_rs, lora_b, b_rs, true, y, y_rs, w, st)) != MGA_OK) return rc;
+  return MGA_OK;
+}
+
+int mga_gated_lora_bwd(const void *grad_y, int64_t gy_rs, const void *x, int64_t x_rs, const void *h, int64_t h_rs,
+                       const void *weight, int64_t w_rs, const void *lora_a, int64_t a_rs, const void *lora_b,
+                       int64_t b_rs, const void *t, int64_t t_rs, const float *gate, float scaling, double dropout_p,
+                       uint64_t seed, int32_t S, int32_t K, int32_t N, int32_t rank, void *grad_x, int64_t gx_rs,
+                       void *grad_a, int64_t ga_rs, void *grad_b, int64_t gb_rs, void *workspace,
+                       int64_t workspace_bytes, void *stream) {
+  const char *fn = "mga_gated_lora_bwd";
+  int rc;
+  if ((rc = check_lora_sizes(fn, S, K, N, rank, dropout_p)) != MGA_OK) return rc;
+  const uint32_t thr = drop_threshold(dropout_p);
+  const int64_t rp = lora_rpad(rank);
+  if ((rc = check_rows_ld(fn, "grad_output", grad_y, gy_rs, N)) ||
+      (rc = check_rows_ld(fn, "lora_B", lora_b, b_rs, rank)) || (rc = check_rows_ld(fn, "t", t, t_rs, rp)))
+    return rc;
+  if (grad_x && ((rc = check_rows_ld(fn, "weight", weight, w_rs, K)) ||
+                 (rc = check_rows_ld(fn, "lora_A", lora_a, a_rs, K)) ||
+                 (rc = check_rows_ld(fn, "grad_x", grad_x, gx_rs, K))))
+    return rc;
+  if (grad_x && thr && (!aligned16(grad_x) || gx_rs % 4))
+    return fail(MGA_ERR_INVALID, "%s: grad_x must be 16-byte aligned with a row stride multiple of 4", fn);
+  if (grad_a && ((rc = check_rows_ld(fn, "grad_A", grad_a, ga_rs, K)) ||
+                 (rc = check_rows_ld(fn, thr ? "dropout output h" : "x", thr ? h : x, thr ? h_rs : x_rs, K))))
+    return rc;
+  if (grad_b && (rc = check_rows_ld(fn, "grad_B", grad_b, gb_rs, rank))) return rc;
+  if (!workspace || workspace_bytes < lora_ws_bytes(S, K, rank))
+    return fail(MGA_ERR_INVALID, "%s: workspace of %lld bytes needed", fn, (long long)lora_ws_bytes(S, K, rank));
+  const LoraWs w = lora_ws(workspace, S, rank);
+  hipStream_t st = (hipStream_t)stream;
+  // u = dY B, d_a = T(T(u gate) s)  (the gradient at lora_A's output)
+  if ((rc = blas(fn, false, false, S, rank, N, grad_y, gy_rs, lora_b, b_rs, false, w.u, rp, w, st)) != MGA_OK)
+    return rc;
+  mga::launch_lora_scale_rows(w.u, rp, gate, scaling, S, rank, (int32_t)rp, w.da, rp, st);
+  if ((rc = check_launch(fn)) != MGA_OK) return rc;
+  // dB = dY^T t
+  if (grad_b && (rc = blas(fn, true, false, N, rank, S, grad_y, gy_rs, t, t_rs, false, grad_b, gb_rs, w, st)))
+    return rc;
+  if (grad_x) {
+    // dX = dY W, then the LoRA path through dropout
+    if ((rc = blas(fn, false, false, S, K, N, grad_y, gy_rs, weight, w_rs, false, grad_x, gx_rs, w, st)) != MGA_OK)
+      return rc;
+    if (thr) {
+      mga::launch_lora_transpose(lora_a, a_rs, rank, K, (int32_t)rp, w.at, rp, st);
+      mga::LoraDxArgs d = {};
+      d.da = w.da; d.da_rs = rp; d.At = w.at; d.at_rs = rp; d.dx = grad_x; d.dx_rs = gx_rs;
+      d.keep_scale = keep_scale(dropout_p); d.thr = thr; d.seed = seed; d.S = S; d.K = K; d.rank = rank;
+      mga::launch_lora_dx(d, st);
+      if ((rc = check_launch(fn)) != MGA_OK) return rc;
+    } else if ((rc = blas(fn, false, false, S, K, rank, w.da, rp, lora_a, a_rs, true, grad_x, gx_rs, w, st))) {
+      return rc;
+    }
+  }
+  // dA = d_a^T dropout(x)
+  if (grad_a && (rc = blas(fn, true, false, rank, K, S, w.da, rp, thr ? h : x, thr ? h_rs : x_rs, false, grad_a,
+                           ga_rs, w, st)))
+    return rc;
+  return MGA_OK;
 }
 
 int64_t mga_soft_ce_workspace_floats(int32_t n_rows, int32_t n_cols) {

@@ -66,6 +66,41 @@ struct QkRopeArgs {
 };
 void launch_qk_norm_rope(const QkRopeArgs &a, bool is_f32, bool backward, hipStream_t stream);
 
+// Plain bf16 GEMM through hipBLASLt, row-major (mga_blas.hip):
+// D[M, N] = op(A)[M, K] op(B)[K, N] (+ D), op(A) = A^T when ta (A stored
+// [K, M]), op(B) = B^T when tb (B stored [N, K]). Returns 0, or -1 with *err set.
+int gemm_bf16(bool ta, bool tb, int64_t M, int64_t N, int64_t K, const void *A, int64_t lda, const void *B,
+              int64_t ldb, bool accumulate, void *D, int64_t ldd, void *workspace, size_t ws_bytes,
+              hipStream_t stream, const char **err);
+
+// Gated LoRA kernels (mga_lora.hip).
+struct LoraDownArgs {
+  const void *x; int64_t x_rs;         // [S, K] bf16
+  const void *A; int64_t a_rs;         // lora_A weight [rank, K]
+  const float *gate;                   // [S] or null (= 1)
+  float scaling, keep_scale;           // alpha / rank; 1 / (1 - p)
+  uint32_t thr;                        // 16-bit drop threshold, 0 = no dropout
+  uint64_t seed;
+  void *h; int64_t h_rs;               // dropout output [S, K] (thr > 0)
+  void *t; int64_t t_rs;               // [S, rpad] bf16 out
+  int32_t S, K, rank;
+};
+struct LoraDxArgs {
+  const void *da; int64_t da_rs;       // [S, rpad] bf16
+  const void *At; int64_t at_rs;       // [K, rpad] bf16
+  void *dx; int64_t dx_rs;             // [S, K] bf16, updated in place
+  float keep_scale;
+  uint32_t thr;
+  uint64_t seed;
+  int32_t S, K, rank;
+};
+void launch_lora_down(const LoraDownArgs &a, hipStream_t stream);
+void launch_lora_dx(const LoraDxArgs &a, hipStream_t stream);
+void launch_lora_scale_rows(const void *u, int64_t u_rs, const float *gate, float scaling, int32_t S,
+                            int32_t rank, int32_t rpad, void *da, int64_t da_rs, hipStream_t stream);
+void launch_lora_transpose(const void *A, int64_t a_rs, int32_t rank, int32_t K, int32_t rpad, void *At,
+                           int64_t at_rs, hipStream_t stream);
+
 // Stable soft cross-entropy (mga_soft_ce.hip). Rows of V columns; row strides
 // in elements; vec: 16-byte vector loads (every row start 16-byte aligned).
 int64_t soft_ce_workspace_floats(int32_t n_rows, int32_t n_cols);

@@ -1,0 +1,166 @@
+"""HIP / hipBLASLt gated LoRA layer (mga_gated_lora_*) against the float64
+oracle (oracle/gated_lora.py, pinned by tests/test_oracle_gated_lora.py) on the
+same bf16 inputs, the mask included.
+
+Tolerances follow the bf16 roundings on each path (u = 2^-8 covers two
+roundings of 2^-9):
+* y: the base product is rounded, then the rank-r term (whose activations t
+  are rounded) is added and the sum rounded:
+  |y - y*| <= u (|y*| + |x W^T| + s g |h A^T| |B|^T) + 1e-5 max|y*|;
+* dX: the base gradient dY W is rounded, the LoRA term goes through three
+  roundings (u = dY B, d_a A, the dropout scaling) and the sum is rounded:
+  |dX - dX*| <= u (|dX*| + |dY W| + 2 |d_a| |A| / (1 - p)) + 1e-5 max|dX*|;
+* dA = d_a^T h and dB = dY^T t (sums over the S rows of rounded factors):
+  |d - d*| <= u (|d*| + |a|^T |b|) with |a|^T |b| the sum of absolute products;
+* the dropout output h equals the oracle's keep mask times T(x / (1 - p)) bit
+  for bit.
+The full Qwen3-8B qkv shape (S = 5120) is compared with an fp32 torch
+reference on the GPU under the same bounds.
+"""
+import importlib
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import gated_lora as gl
+
+pytestmark = pytest.mark.gpu
+U = 2.0 ** -8
+
+
+def lora_mod():
+    return importlib.import_module("mtp-glora_amd.lora")
+
+
+def make(S, K, N, r, dev, seed=0, gate="mixed"):
+    g = torch.Generator(device=dev).manual_seed(seed)
+    x = torch.randn(S, K, generator=g, device=dev).bfloat16()
+    W = (torch.randn(N, K, generator=g, device=dev) / K ** 0.5).bfloat16()
+    A = (torch.randn(r, K, generator=g, device=dev) / K ** 0.5).bfloat16()
+    B = (torch.randn(N, r, generator=g, device=dev) * (0.5 / r ** 0.5)).bfloat16()
+    gt = None if gate is None else (torch.rand(S, generator=g, device=dev) < 0.7).float()
+    return x, W, A, B, gt
+
+
+def f64(t):
+    return None if t is None else t.detach().double().cpu().numpy()
+
+
+def check(name, got, ref, bound):
+    err = np.abs(got - ref)
+    worst = (err / bound).max()
+    print(f"  {name}: max-abs {err.max():.3e}, worst err/bound {worst:.3f}", flush=True)
+    assert worst <= 1.0, name
+
+
+def run_case(dev, S, K, N, r, p, gate="mixed", seed=0, scaling=2.0):
+    lm = lora_mod()
+    x, W, A, B, gt = make(S, K, N, r, dev, seed, gate)
+    sd = 1234567 + seed
+    y, t, h = lm.gated_lora_forward(x, W, A, B, gt, scaling, p, sd)
+    dy = torch.randn(S, N, generator=torch.Generator(device=dev).manual_seed(seed + 7), device=dev).bfloat16()
+    gx, ga, gb = lm.gated_lora_backward(dy, x, h, t, W, A, B, gt, scaling, p, sd, True, True, True)
+    torch.cuda.synchronize()
+    X, Wn, An, Bn, G, DY = f64(x), f64(W), f64(A), f64(B), f64(gt), f64(dy)
+    keep = gl.keep_mask(sd, S, K, p) if p > 0 else None
+    if p > 0:   # the kernel's dropout output, bit for bit
+        want = (keep * f64(x.float().mul(1.0 / (1.0 - p)).bfloat16()))
+        np.testing.assert_array_equal(f64(h), want)
+    Gv = np.ones(S) if G is None else G
+    H = X if keep is None else X * keep / (1 - p)
+    ks = 1.0 if p == 0 else 1.0 / (1 - p)
+    y_ref = gl.forward(X, Wn, An, Bn, G, scaling, keep, p)
+    lora_abs = scaling * Gv[:, None] * (np.abs(H @ An.T) @ np.abs(Bn).T)
+    check("y", f64(y), y_ref, U * (np.abs(y_ref) + np.abs(X @ Wn.T) + lora_abs) + 1e-5 * np.abs(y_ref).max())
+    dx_ref, dA_ref, dB_ref = gl.backward(DY, X, Wn, An, Bn, G, scaling, keep, p)
+    d_a = scaling * Gv[:, None] * (DY @ Bn)
+    bx = U * (np.abs(dx_ref) + np.abs(DY @ Wn) + 2 * ks * (np.abs(d_a) @ np.abs(An))) + 1e-5 * np.abs(dx_ref).max()
+    check("dX", f64(gx), dx_ref, bx)
+    check("dA", f64(ga), dA_ref, U * (np.abs(dA_ref) + np.abs(d_a).T @ np.abs(H)) + 1e-30)
+    T = scaling * Gv[:, None] * (H @ An.T)
+    check("dB", f64(gb), dB_ref, U * (np.abs(dB_ref) + np.abs(DY).T @ np.abs(T)) + 1e-30)
+    return y, t, h
+
+
+@pytest.mark.parametrize("p", [0.0, 0.05])
+def test_qwen3_qkv_shape(dev, p):
+    """Qwen3-8B fused qkv_proj with the reference's training ranks (3 x 32)."""
+    run_case(dev, S=512, K=4096, N=6144, r=96, p=p)
+
+
+@pytest.mark.parametrize("S,K,N,r,p,gate", [
+    (333, 4096, 4096, 32, 0.05, None),      # o_proj-like, ragged rows, no gate
+    (100, 256, 256, 8, 0.0, "mixed"),       # config-1 sizes
+    (64, 512, 384, 160, 0.1, "mixed"),      # rank above 96: chunked down-projection
+    (40, 1024, 200, 64, 0.5, "mixed"),      # gate_up-like rank, heavy dropout, odd N
+    (31, 128, 64, 1, 0.0, "mixed"),         # rank 1, one partial row block
+])
+def test_shapes(dev, S, K, N, r, p, gate):
+    run_case(dev, S, K, N, r, p, gate=gate, seed=S)
+
+
+def test_full_qkv_forward_against_fp32(dev):
+    """S = 5120 (config 2's chunk): forward against torch fp32 on the GPU."""
+    lm = lora_mod()
+    S, K, N, r, p, s = 5120, 4096, 6144, 96, 0.05, 2.0
+    x, W, A, B, gt = make(S, K, N, r, dev, seed=3)
+    y, t, h = lm.gated_lora_forward(x, W, A, B, gt, s, p, 99)
+    hf, xf, Wf, Af, Bf = h.float(), x.float(), W.float(), A.float(), B.float()
+    base = xf @ Wf.T
+    lora = s * gt[:, None] * ((hf @ Af.T) @ Bf.T)
+    ref = base + lora
+    lora_abs = s * gt[:, None] * ((hf @ Af.T).abs() @ Bf.abs().T)
+    bound = U * (ref.abs() + base.abs() + lora_abs) + 1e-5 * ref.abs().max()
+    worst = ((y.float() - ref).abs() / bound).max().item()
+    kept = (h != 0).float().mean().item()
+    print(f"  S=5120: worst err/bound {worst:.3f}, kept fraction {kept:.4f}", flush=True)
+    assert worst <= 1.0
+    assert abs(kept - (1 - gl.drop_threshold(p) / 65536)) < 1e-3
+
+
+def test_module_forward_backward(dev):
+    """GatedLoRALinear (the mirror) in train mode through autograd: x, lora_A
+    and lora_B get gradients, the base weight none, and the result equals the
+    functional entry points with the same seed."""
+    lm = lora_mod()
+    torch.manual_seed(0)
+    base = torch.nn.Linear(256, 384, bias=False).to(dev, torch.bfloat16)
+    layer = lm.GatedLoRALinear(base, rank=16, alpha=32, dropout=0.05, lora_bias=False, use_rslora=False)
+    base.weight.requires_grad_(False)
+    with torch.no_grad():
+        layer.lora_B.weight.normal_(0, 0.05)
+    x = torch.randn(1, 100, 256, device=dev).bfloat16().requires_grad_()
+    gate = (torch.rand(1, 100, 1, device=dev) < 0.5).long()
+    torch.manual_seed(5)
+    y = layer(x, gate)
+    y.float().square().sum().backward()
+    assert y.shape == (1, 100, 384) and y.dtype == torch.bfloat16
+    assert x.grad is not None and layer.lora_A.weight.grad is not None and layer.lora_B.weight.grad is not None
+    assert base.weight.grad is None
+    torch.manual_seed(5)
+    seed = int(torch.randint(0, 2 ** 62, (), dtype=torch.int64).item())
+    y2, _, _ = lm.gated_lora_forward(x.detach()[0], base.weight, layer.lora_A.weight, layer.lora_B.weight,
+                                     gate.reshape(-1).float(), 2.0, 0.05, seed)
+    assert torch.equal(y.detach()[0], y2)
+    layer.eval()
+    y3 = layer(x.detach(), gate)
+    y4, _, _ = lm.gated_lora_forward(x.detach()[0], base.weight, layer.lora_A.weight, layer.lora_B.weight,
+                                     gate.reshape(-1).float(), 2.0, 0.0, 0)
+    assert torch.equal(y3[0], y4)
+
+
+def test_argument_errors(dev):
+    lm = lora_mod()
+    x, W, A, B, gt = make(8, 64, 32, 4, dev)
+    with pytest.raises(TypeError):
+        lm.gated_lora_linear(x.float(), W, A, B, gt, 2.0)
+    with pytest.raises(NotImplementedError):
+        lm.gated_lora_linear(x, W.clone().requires_grad_(), A, B, gt, 2.0)
+    with pytest.raises(ValueError):
+        lm.gated_lora_linear(x, W, A, B, gt[:5], 2.0)
+    x2, W2, A2, B2, g2 = make(8, 40, 32, 4, dev)
+    with pytest.raises(Exception, match="multiple of 16"):
+        lm.gated_lora_linear(x2, W2, A2, B2, g2, 2.0)
+    with pytest.raises(RuntimeError):
+        lm.gated_lora_linear(x.cpu(), W.cpu(), A.cpu(), B.cpu(), None, 2.0)
