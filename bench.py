@@ -228,6 +228,66 @@ def qk_rope_phase(torch, timer, S: int, Hq: int, Hkv: int, D: int, n: int, cpu_t
                           f"median of 3 after a warm-up, {torch.get_num_threads()} threads"}
 
 
+def gated_lora_phase(torch, timer, S: int, K: int, N: int, rank: int, p: float, n: int, cpu_rows: int) -> dict:
+    """The gated LoRA layer (GatedLoRALinear, gated_lora.py:51-53) at Qwen3-8B's
+    fused qkv_proj with the reference's training ranks and dropout: forward and
+    backward of the fused layer, the base GEMM alone (the floor any layout
+    pays), and the reference's torch ops on the same GPU and on the CPU."""
+    from importlib import import_module
+    lm = import_module("mtp-glora_amd.lora")
+    F = torch.nn.functional
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(SEED + 11)
+    bf = torch.bfloat16
+    x = torch.randn(S, K, generator=g, device=dev).to(bf)
+    W = (torch.randn(N, K, generator=g, device=dev) / K ** 0.5).to(bf)
+    A = (torch.randn(rank, K, generator=g, device=dev) / K ** 0.5).to(bf)
+    B = (torch.randn(N, rank, generator=g, device=dev) * 0.05).to(bf)
+    gate = (torch.rand(S, generator=g, device=dev) < 0.8).float()
+    dy = torch.randn(S, N, generator=g, device=dev).to(bf)
+    scaling = 2.0
+    y, t, h = lm.gated_lora_forward(x, W, A, B, gate, scaling, p, 7)
+    t_f = timer(lambda: lm.gated_lora_forward(x, W, A, B, gate, scaling, p, 7), n)
+    t_b = timer(lambda: lm.gated_lora_backward(dy, x, h, t, W, A, B, gate, scaling, p, 7, True, True, True), n)
+    t_gemm = timer(lambda: F.linear(x, W), n)
+
+    def reference(xx, go):
+        # GatedLoRALinear.forward as the reference runs it, then autograd
+        xr = xx.detach().requires_grad_()
+        Ar, Br = A.detach().requires_grad_(), B.detach().requires_grad_()
+        out = F.linear(xr, W) + scaling * F.linear(F.linear(F.dropout(xr, p, True), Ar), Br) * gate[:xx.shape[0], None]
+        out.backward(go)
+
+    t_ref = timer(lambda: reference(x, dy), n)
+    fl_fwd = 2.0 * S * K * N + 2.0 * S * rank * (K + N)
+    fl_bwd = 2.0 * S * K * N + 4.0 * S * rank * (K + N)
+    xc, dyc = x[:cpu_rows].cpu(), dy[:cpu_rows].cpu()
+    W_c, A_c, B_c, g_c = W.cpu(), A.cpu(), B.cpu(), gate.cpu()
+    secs = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        xr = xc.detach().requires_grad_()
+        Ar, Br = A_c.detach().requires_grad_(), B_c.detach().requires_grad_()
+        out = F.linear(xr, W_c) + scaling * F.linear(F.linear(F.dropout(xr, p, True), Ar), Br) * g_c[:cpu_rows, None]
+        out.backward(dyc)
+        secs.append(time.perf_counter() - t0)
+    cpu_s = sorted(secs[1:])[0]
+    # HIP kernels' algorithmic bytes: the down-projection reads x and writes
+    # the dropout output (+ t); the dX update reads and writes dX
+    down_bytes = S * K * 2 * (2 if p > 0 else 1) + S * ((rank + 31) // 32 * 32) * 2
+    dx_bytes = 2 * S * K * 2 if p > 0 else 0
+    return {"S": S, "in": K, "out": N, "rank": rank, "dropout": p, "dtype": "bf16",
+            "fwd_ms": round(t_f, 4), "bwd_ms": round(t_b, 4), "base_gemm_ms": round(t_gemm, 4),
+            "fwd_tflops": round(fl_fwd / (t_f * 1e-3) / 1e12, 1), "bwd_tflops": round(fl_bwd / (t_b * 1e-3) / 1e12, 1),
+            "base_gemm_tflops": round(2.0 * S * K * N / (t_gemm * 1e-3) / 1e12, 1),
+            "fwd_over_base_gemm": round(t_f / t_gemm, 3),
+            "torch_eager_gpu_fwd_bwd_ms": round(t_ref, 4),
+            "kernel_bytes": {"lora_down_kernel": down_bytes, "lora_dx_kernel": dx_bytes},
+            "cpu_rows_per_s": round(cpu_rows / cpu_s, 1), "gpu_rows_per_s": round(S / ((t_f + t_b) * 1e-3), 1),
+            "cpu_sample": f"the reference's ops as torch eager bf16 on the CPU, fwd + bwd, {cpu_rows} rows, "
+                          f"best of 2 after a warm-up, {torch.get_num_threads()} threads"}
+
+
 def graph_time(torch, fn, n: int, reps: int = 5) -> float:
     """Average duration of ``fn`` captured ``n`` times into one HIP graph
     (removes host launch gaps from microsecond kernels)."""
@@ -351,6 +411,16 @@ def pmc_pass(torch, mga, libc, q, k, v, do, kp, cache, chunk0, P, S, R, Hkv, D, 
     _, _, rs_ = rope.norm_rope_forward(qr_, kr_, wr_, wr_, cr_, cr_, 1e-6)
     gq_, gk_ = torch.randn_like(qr_), torch.randn_like(kr_)   # gradients: their own memory
     rope.norm_rope_backward(qr_, kr_, wr_, wr_, cr_, cr_, rs_, gq_, gk_)
+    lm = importlib.import_module("mtp-glora_amd.lora")
+    Kl, Nl = Hq * D, (Hq + 2 * Hkv) * D
+    xl = torch.randn(S, Kl, device=dev).bfloat16()
+    Wl = torch.randn(Nl, Kl, device=dev).bfloat16()
+    Al = torch.randn(96, Kl, device=dev).bfloat16()
+    Bl = torch.randn(Nl, 96, device=dev).bfloat16()
+    gl_ = torch.ones(S, device=dev)
+    _, tl, hl = lm.gated_lora_forward(xl, Wl, Al, Bl, gl_, 2.0, 0.05, 7)
+    lm.gated_lora_backward(torch.randn(S, Nl, device=dev).bfloat16(), xl, hl, tl, Wl, Al, Bl, gl_, 2.0, 0.05, 7,
+                           True, True, True)
     torch.cuda.synchronize()
     calib = Hkv * CALIB_ROWS * D * 2 * 2
     print(json.dumps({"pmc_pass": True, "calibration": {"kernel": "kv_copy_rows_kernel",
@@ -574,6 +644,7 @@ def main() -> int:
               "append_commit": t_commit, "append_stage": t_stage}
     soft_ce = soft_ce_phase(torch, mga, timer, int(anchors.numel()), QWEN3_VOCAB, n, cpu_rows=16)
     qk_rope = qk_rope_phase(torch, timer, S, Hq, Hkv, D, n, cpu_tokens=256)
+    lora = gated_lora_phase(torch, timer, S, Hq * D, (Hq + 2 * Hkv) * D, 96, 0.05, n, cpu_rows=32)
     traffic = load_traffic(args.traffic, args.config)
     credited = {"fwd": fl_fwd, "bwd_dq_pass": fl_dq, "bwd_dkdv_pass": fl_dkdv}
     dom = max(credited, key=lambda kname: phases[kname])
@@ -617,6 +688,7 @@ def main() -> int:
                               if traffic else None),
         "soft_ce": soft_ce,
         "qk_norm_rope": qk_rope,
+        "gated_lora_qkv": lora,
         "host_ms_per_step": round(host_ms, 4),
     }
 

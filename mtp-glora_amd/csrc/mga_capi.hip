@@ -270,15 +270,18 @@ int64_t lora_rpad(int32_t rank) { return (rank + 31) / 32 * 32; }
 
 struct LoraWs {
   void *blas, *u, *da, *at;
+  float *part;
 };
 
-// [hipBLASLt workspace | u = dY B : S x rpad | d_a : S x rpad | A^T : K x rpad], bf16
+// [hipBLASLt workspace | u = dY B : S x rpad | d_a : S x rpad | A^T : K x rpad
+//  (bf16) | split-K partial sums of the down-projection: 8 x S x 96 fp32]
 int64_t lora_ws_bytes(int32_t S, int32_t K, int32_t rank) {
   const int64_t rp = lora_rpad(rank);
-  return kBlasWorkspace + 2 * align256((int64_t)S * rp * 2) + align256((int64_t)K * rp * 2);
+  return kBlasWorkspace + 2 * align256((int64_t)S * rp * 2) + align256((int64_t)K * rp * 2) +
+         align256((int64_t)8 * S * 96 * 4);
 }
 
-LoraWs lora_ws(void *ws, int32_t S, int32_t rank) {
+LoraWs lora_ws(void *ws, int32_t S, int32_t K, int32_t rank) {
   const int64_t rp = lora_rpad(rank);
   char *p = static_cast<char *>(ws);
   LoraWs w;
@@ -286,6 +289,7 @@ LoraWs lora_ws(void *ws, int32_t S, int32_t rank) {
   w.u = p + kBlasWorkspace;
   w.da = static_cast<char *>(w.u) + align256((int64_t)S * rp * 2);
   w.at = static_cast<char *>(w.da) + align256((int64_t)S * rp * 2);
+  w.part = reinterpret_cast<float *>(static_cast<char *>(w.at) + align256((int64_t)K * rp * 2));
   return w;
 }
 
@@ -350,7 +354,7 @@ int mga_gated_lora_fwd(const void *x, int64_t x_rs, const void *weight, int64_t 
   if (thr > 0 && (rc = check_vec_rows(fn, "dropout output h", h, h_rs, K)) != MGA_OK) return rc;
   if (!workspace || workspace_bytes < lora_ws_bytes(S, K, rank))
     return fail(MGA_ERR_INVALID, "%s: workspace of %lld bytes needed", fn, (long long)lora_ws_bytes(S, K, rank));
-  const LoraWs w = lora_ws(workspace, S, rank);
+  const LoraWs w = lora_ws(workspace, S, K, rank);
   hipStream_t st = (hipStream_t)stream;
   // y = x W^T
   if ((rc = blas(fn, false, true, S, N, K, x, x_rs, weight, w_rs, false, y, y_rs, w, st)) != MGA_OK) return rc;
@@ -358,7 +362,7 @@ int mga_gated_lora_fwd(const void *x, int64_t x_rs, const void *weight, int64_t 
   mga::LoraDownArgs a = {};
   a.x = x; a.x_rs = x_rs; a.A = lora_a; a.a_rs = a_rs; a.gate = gate; a.scaling = scaling;
   a.keep_scale = keep_scale(dropout_p); a.thr = thr; a.seed = seed; a.h = thr ? h : nullptr; a.h_rs = h_rs;
-  a.t = t; a.t_rs = t_rs; a.S = S; a.K = K; a.rank = rank;
+  a.t = t; a.t_rs = t_rs; a.part = w.part; a.S = S; a.K = K; a.rank = rank;
   mga::launch_lora_down(a, st);
   if ((rc = check_launch(fn)) != MGA_OK) return rc;
   // y += t B^T
@@ -392,7 +396,7 @@ int mga_gated_lora_bwd(const void *grad_y, int64_t gy_rs, const void *x, int64_t
   if (grad_b && (rc = check_rows_ld(fn, "grad_B", grad_b, gb_rs, rank))) return rc;
   if (!workspace || workspace_bytes < lora_ws_bytes(S, K, rank))
     return fail(MGA_ERR_INVALID, "%s: workspace of %lld bytes needed", fn, (long long)lora_ws_bytes(S, K, rank));
-  const LoraWs w = lora_ws(workspace, S, rank);
+  const LoraWs w = lora_ws(workspace, S, K, rank);
   hipStream_t st = (hipStream_t)stream;
   // u = dY B, d_a = T(T(u gate) s)  (the gradient at lora_A's output)
   if ((rc = blas(fn, false, false, S, rank, N, grad_y, gy_rs, lora_b, b_rs, false, w.u, rp, w, st)) != MGA_OK)

@@ -7,15 +7,21 @@
 // output, dY W, dY B, dY^T t, d_a^T h) go to hipBLASLt (mga_blas.hip). The
 // kernels here fuse what a library GEMM cannot:
 //
-// * lora_down_kernel: t = T(T(s * T(h A^T)) * gate) for every row, h =
+// * the down-projection t = T(T(s * T(h A^T)) * gate) for every row, h =
 //   dropout(x) drawn on the fly (and written out when dropout is on: the
 //   backward's dA GEMM reads it, as the reference keeps its dropout output).
-//   HBM-bound on x: 32 rows per workgroup, the K dimension split over 8 waves
-//   (v_mfma_f32_32x32x16_bf16, operands straight from global memory), the
-//   partial sums reduced through LDS.
+//   HBM-bound on x; v_mfma_f32_32x32x16_bf16 with 32 rows per workgroup.
+//   lora_down_lds_kernel (K a multiple of 128) copies 128-wide chunks of the
+//   x rows and of A into LDS with direct loads (1 KB per instruction) and
+//   splits K over up to 8 workgroups per row block, whose fp32 partial sums
+//   lora_down_finish_kernel adds in a fixed order; lora_down_kernel (other K)
+//   reads its operands straight from global memory, K split over 8 waves.
+//   Operand loads that give each lane its own row touch 32 cache lines per
+//   instruction; staging through LDS is what makes the first variant faster.
 // * lora_dx_kernel (dropout on): dX = T(dX + T(mask * scale * T(d_a A))) in
 //   place over the base gradient dY W: HBM-bound on dX, the rank-r product on
-//   MFMA with the output's columns along each lane's four rows.
+//   MFMA with the output's columns along each lane's four rows; every load
+//   issued before the first MFMA.
 // * lora_scale_rows_kernel: d_a = T(T(u * gate) * s), u = dY B.
 // * lora_transpose_kernel: A^T padded to a multiple of 32 ranks (the dX
 //   kernel's MFMA operand wants rank-contiguous rows).
@@ -32,6 +38,8 @@
 // bits & 0xffff >= thr, element 2j + 1 when bits >> 16 >= thr, thr =
 // round(p * 65536). Kept elements are multiplied by 1 / (1 - p), as
 // torch's dropout does. The backward draws the same bits again.
+#include <type_traits>
+
 #include "mga_common.hpp"
 #include "mga_internal.hpp"
 
@@ -62,37 +70,42 @@ __device__ __forceinline__ bf16x8 zero8() {
 }
 
 constexpr int kDownWaves = 8;
+constexpr int kDownMaxSplit = 8;   // split-K parts of the LDS down-projection (partials: 8 x S x 96 fp32)
 
 }  // namespace
 
 // Grid: ceil(S / 32) workgroups of 8 waves. Wave w takes the 16-wide k steps
 // w, w + 8, ... of the workgroup's 32 rows; NB = ranks / 32 accumulator blocks.
+// Loads are unconditional (rows past S and ranks past the rank read a clamped,
+// valid address; their sums land only in outputs that are dropped or zeroed)
+// and issued kU steps ahead of the MFMAs that use them.
 template <int NB, bool DROP>
 __global__ __launch_bounds__(kDownWaves * 64) void lora_down_kernel(LoraDownArgs a) {
+  constexpr int kU = NB >= 3 ? 4 : 8;
   const int w = wave_id(), lane = threadIdx.x & 63;
   const int s0 = blockIdx.x * 32;
   const int row = s0 + (lane & 31);
   const bool row_ok = row < a.S;
+  const int rowc = row_ok ? row : a.S - 1;
   const int kq = 8 * (lane >> 5);
-  const bf16_t *xr = reinterpret_cast<const bf16_t *>(a.x) + (int64_t)(row_ok ? row : 0) * a.x_rs + kq;
-  bf16_t *hr = (DROP && a.h) ? reinterpret_cast<bf16_t *>(a.h) + (int64_t)(row_ok ? row : 0) * a.h_rs + kq : nullptr;
+  const bf16_t *xr = reinterpret_cast<const bf16_t *>(a.x) + (int64_t)rowc * a.x_rs + kq;
+  bf16_t *hr = (DROP && a.h) ? reinterpret_cast<bf16_t *>(a.h) + (int64_t)rowc * a.h_rs + kq : nullptr;
   const bf16_t *ar[NB];
-  bool a_ok[NB];
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
     const int r = nb * 32 + (lane & 31);
-    a_ok[nb] = r < a.rank;
-    ar[nb] = reinterpret_cast<const bf16_t *>(a.A) + (int64_t)(a_ok[nb] ? r : 0) * a.a_rs + kq;
+    ar[nb] = reinterpret_cast<const bf16_t *>(a.A) + (int64_t)(r < a.rank ? r : a.rank - 1) * a.a_rs + kq;
   }
   f32x16 acc[NB];
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) acc[nb] = zero16();
-  const uint64_t pair0 = ((uint64_t)(row_ok ? row : 0) * (uint64_t)a.K + (uint64_t)kq) >> 1;
+  const uint64_t pair0 = ((uint64_t)rowc * (uint64_t)a.K + (uint64_t)kq) >> 1;
+  const int nsteps = (a.K / 16 - w + kDownWaves - 1) / kDownWaves;   // wave-uniform
 
-#pragma unroll 4
-  for (int k0 = 16 * w; k0 < a.K; k0 += 16 * kDownWaves) {
-    bf16x8 xv = row_ok ? load8(xr + k0) : zero8();
+  // one k step: dropout on the x operand (h written out), then the MFMAs
+  auto consume = [&](bf16x8 &xv, const bf16x8 (&av)[NB], int step) {
     if constexpr (DROP) {
+      const int k0 = 16 * (w + kDownWaves * step);
       const uint64_t pj = pair0 + ((uint64_t)k0 >> 1);
 #pragma unroll
       for (int e = 0; e < 8; e += 2) {
@@ -104,10 +117,29 @@ __global__ __launch_bounds__(kDownWaves * 64) void lora_down_kernel(LoraDownArgs
       if (row_ok && hr) *reinterpret_cast<i32x4 *>(hr + k0) = __builtin_bit_cast(i32x4, xv);
     }
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      const bf16x8 av = a_ok[nb] ? load8(ar[nb] + k0) : zero8();
-      acc[nb] = mfma32(xv, av, acc[nb]);
-    }
+    for (int nb = 0; nb < NB; ++nb) acc[nb] = mfma32(xv, av[nb], acc[nb]);
+  };
+  auto load_step = [&](bf16x8 &xv, bf16x8 (&av)[NB], int step) {
+    const int k0 = 16 * (w + kDownWaves * step);
+    xv = load8(xr + k0);
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) av[nb] = load8(ar[nb] + k0);
+  };
+
+  // full groups of kU steps: all loads of a group issued before its MFMAs,
+  // with no branch in between
+  const int nfull = nsteps / kU * kU;
+  for (int i = 0; i < nfull; i += kU) {
+    bf16x8 xv[kU], av[kU][NB];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) load_step(xv[u], av[u], i + u);
+#pragma unroll
+    for (int u = 0; u < kU; ++u) consume(xv[u], av[u], i + u);
+  }
+  for (int i = nfull; i < nsteps; ++i) {
+    bf16x8 xv, av[NB];
+    load_step(xv, av, i);
+    consume(xv, av, i);
   }
 
   // fixed-order reduction of the 8 waves' partial sums: 4..7 into 0..3, then 1..3 into 0
@@ -149,51 +181,224 @@ __global__ __launch_bounds__(kDownWaves * 64) void lora_down_kernel(LoraDownArgs
     for (int nb = 0; nb < NB; ++nb) {
       const int r = nb * 32 + (lane & 31);
       // lora_A output in bf16, then the scaling and the gate, each rounded
-      t[(int64_t)s * a.t_rs + r] = (bf16_t)(rnd(rnd(acc[nb][q]) * a.scaling) * g);
+      const float v = r < a.rank ? rnd(rnd(acc[nb][q]) * a.scaling) * g : 0.f;
+      t[(int64_t)s * a.t_rs + r] = (bf16_t)v;
     }
   }
 }
 
+// LDS-staged variant for K a multiple of 128. Grid: ceil(S / 32) workgroups
+// of 4 waves; chunks of 128 k of the 32 x rows and of the 32 NB rows of A are
+// copied global -> LDS by direct loads (1 KB per instruction, swizzled rows),
+// double-buffered in named buffers; wave w takes k steps 2w, 2w + 1 of each
+// chunk, its MFMA operands read from LDS. The waves' partial sums are reduced
+// in a fixed order through the (then idle) A buffers.
+template <int NB, bool DROP>
+__global__ __launch_bounds__(256) void lora_down_lds_kernel(LoraDownArgs a) {
+  constexpr int HD = 128, NRA = 32 * NB;
+  __shared__ __attribute__((aligned(16))) bf16_t sX0[32 * HD], sX1[32 * HD];
+  __shared__ __attribute__((aligned(16))) bf16_t sA0[NRA * HD], sA1[NRA * HD];
+  const int w = wave_id(), lane = threadIdx.x & 63;
+  const int l32 = lane & 31, hi = lane >> 5;
+  const int s0 = blockIdx.x * 32;
+  const int row = s0 + l32;
+  const bool row_ok = row < a.S;
+  const int nrows = a.S - s0 < 32 ? a.S - s0 : 32;
+  const bf16_t *xb = reinterpret_cast<const bf16_t *>(a.x) + (int64_t)s0 * a.x_rs;
+  const bf16_t *ab = reinterpret_cast<const bf16_t *>(a.A);
+  DmaLane<HD, 32> dx;
+  DmaLane<HD, NRA> da;
+  dx.init();
+  da.init();
+  const uint32_t lrx = dx.lane_row(a.x_rs), lra = da.lane_row(a.a_rs);
+  // operand of k step ks: row l32 (+ 32 nb), granule (2 ks + hi) ^ swz(l32)
+  const uint32_t orow = opaque_u32((uint32_t)(l32 * HD + (((uint32_t)hi ^ swz<HD>(l32)) << 3)) * 2u);
+  bf16_t *hr = (DROP && a.h) ? reinterpret_cast<bf16_t *>(a.h) + (int64_t)(row_ok ? row : 0) * a.h_rs : nullptr;
+  const uint64_t prow = (uint64_t)(row_ok ? row : 0) * (uint64_t)a.K;
+  // this workgroup's share of the K chunks (split K: gridDim.y parts)
+  const int nall = a.K / HD;
+  const int cbeg = (int)((int64_t)nall * blockIdx.y / gridDim.y);
+  const int nchunks = (int)((int64_t)nall * (blockIdx.y + 1) / gridDim.y) - cbeg;
+
+  auto issue = [&](int c, bf16_t *tx, bf16_t *ta) {
+    const int col = (cbeg + c) * HD;
+    if (nrows == 32) dx.issue(tx, xb + col, a.x_rs, lrx);
+    else dx.issue_clamped(tx, xb + col, a.x_rs, nrows);
+    if (a.rank == NRA) da.issue(ta, ab + col, a.a_rs, lra);
+    else da.issue_clamped(ta, ab + col, a.a_rs, a.rank);
+  };
+  f32x16 acc[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) acc[nb] = zero16();
+
+  auto step = [&](auto bsel, int c) {
+    constexpr int Bf = decltype(bsel)::value;
+    const bf16_t *tx = Bf ? sX1 : sX0;
+    const bf16_t *ta = Bf ? sA1 : sA0;
+    if (c + 1 < nchunks) issue(c + 1, Bf ? sX0 : sX1, Bf ? sA0 : sA1);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int ks = 2 * w + j;
+      bf16x8 xv = lds_read8(reinterpret_cast<const bf16_t *>(lds_at(tx, orow ^ (uint32_t)(ks << 5))));
+      if constexpr (DROP) {
+        const int k0 = (cbeg + c) * HD + ks * 16 + 8 * hi;
+        const uint64_t pj = (prow + (uint64_t)k0) >> 1;
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+          const uint32_t bits = pair_bits(a.seed, pj + (e >> 1));
+          const bool k_lo = (bits & 0xffffu) >= a.thr, k_hi = (bits >> 16) >= a.thr;
+          xv[e] = k_lo ? (bf16_t)((float)xv[e] * a.keep_scale) : (bf16_t)0.f;
+          xv[e + 1] = k_hi ? (bf16_t)((float)xv[e + 1] * a.keep_scale) : (bf16_t)0.f;
+        }
+        if (row_ok && hr) *reinterpret_cast<i32x4 *>(hr + k0) = __builtin_bit_cast(i32x4, xv);
+      }
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        const bf16x8 av =
+            lds_read8(reinterpret_cast<const bf16_t *>(lds_at(ta + nb * 32 * HD, orow ^ (uint32_t)(ks << 5))));
+        acc[nb] = mfma32(xv, av, acc[nb]);
+      }
+    }
+    if (c + 1 < nchunks) __builtin_amdgcn_s_waitcnt(0);   // this thread's loads of the next chunk landed
+    __syncthreads();
+  };
+
+  if (nchunks > 0) issue(0, sX0, sA0);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  for (int c = 0; c < nchunks; c += 2) {
+    step(std::integral_constant<int, 0>{}, c);
+    if (c + 1 < nchunks) step(std::integral_constant<int, 1>{}, c + 1);
+  }
+
+  // fixed-order reduction: waves 1..3 park their sums in the A buffers, wave 0 adds
+  float *p1 = reinterpret_cast<float *>(sA0), *p2 = reinterpret_cast<float *>(sA0) + NB * 1024;
+  float *p3 = reinterpret_cast<float *>(sA1);
+  if (w > 0) {
+    float *mine = w == 1 ? p1 : (w == 2 ? p2 : p3);
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int q = 0; q < 16; ++q) mine[(nb * 16 + q) * 64 + lane] = acc[nb][q];
+  }
+  __syncthreads();
+  if (w != 0) return;
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      const int o = (nb * 16 + q) * 64 + lane;
+      acc[nb][q] += p1[o] + p2[o] + p3[o];
+    }
+  if (gridDim.y > 1) {   // fp32 partial sums [split][S][32 NB]; lora_down_finish_kernel adds them
+    float *part = a.part + (int64_t)blockIdx.y * a.S * NRA;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      const int s = s0 + 8 * (q >> 2) + 4 * hi + (q & 3);
+      if (s >= a.S) continue;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) part[(int64_t)s * NRA + nb * 32 + l32] = acc[nb][q];
+    }
+    return;
+  }
+  bf16_t *t = reinterpret_cast<bf16_t *>(a.t);
+#pragma unroll
+  for (int q = 0; q < 16; ++q) {
+    const int s = s0 + 8 * (q >> 2) + 4 * hi + (q & 3);
+    if (s >= a.S) continue;
+    const float g = a.gate ? a.gate[s] : 1.f;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      const int r = nb * 32 + l32;
+      const float v = r < a.rank ? rnd(rnd(acc[nb][q]) * a.scaling) * g : 0.f;
+      t[(int64_t)s * a.t_rs + r] = (bf16_t)v;
+    }
+  }
+}
+
+// t[s][r] = T(T(s * T(sum over the splits, in order)) * gate) from the partial
+// sums of the split-K down-projection (ranks nr = 32 NB of this launch).
+__global__ __launch_bounds__(256) void lora_down_finish_kernel(LoraDownArgs a, int nsplit, int nr) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)a.S * nr) return;
+  const int s = (int)(i / nr), r = (int)(i - (int64_t)s * nr);
+  float v = 0.f;
+  for (int k = 0; k < nsplit; ++k) v += a.part[(int64_t)k * a.S * nr + i];
+  const float g = a.gate ? a.gate[s] : 1.f;
+  const float out = r < a.rank ? rnd(rnd(v) * a.scaling) * g : 0.f;
+  reinterpret_cast<bf16_t *>(a.t)[(int64_t)s * a.t_rs + r] = (bf16_t)out;
+}
+
 // Grid: (ceil(K / 512), ceil(S / 32)), 4 waves; wave w covers 32 rows x 128
 // columns of dX. D^T[k][s] = sum_r A^T[k][r] d_a[s][r]; each lane holds one
-// row s and four runs of four consecutive columns per 32-column block.
+// row s and four runs of four consecutive columns per 32-column block. Every
+// load (the lane's dX runs, its d_a row, the A^T rows of its four blocks) is
+// issued before the first MFMA when the rank is at most 16 NK (larger ranks
+// go in chunks of NK steps). d_a and A^T are zero-padded to a multiple of 32
+// ranks, so the step count is even.
+template <int NK>
 __global__ __launch_bounds__(256) void lora_dx_kernel(LoraDxArgs a) {
   const int w = wave_id(), lane = threadIdx.x & 63;
-  const int s = blockIdx.y * 32 + (lane & 31);
+  const int l32 = lane & 31, hi = lane >> 5;
+  const int s = blockIdx.y * 32 + l32;
   const bool s_ok = s < a.S;
-  const int rq = 8 * (lane >> 5);
-  const int nsteps = (a.rank + 15) / 16;   // d_a and A^T are zero-padded to a multiple of 32 ranks
-  const bf16_t *dar = reinterpret_cast<const bf16_t *>(a.da) + (int64_t)(s_ok ? s : 0) * a.da_rs + rq;
-  bf16_t *dxr = reinterpret_cast<bf16_t *>(a.dx) + (int64_t)(s_ok ? s : 0) * a.dx_rs;
+  const int sc = s_ok ? s : a.S - 1;     // clamped rows: their sums are never stored
+  const int rq = 8 * hi;
   const int kb0 = blockIdx.x * 512 + w * 128;
-  for (int blk = 0; blk < 4; ++blk) {
-    const int kbase = kb0 + blk * 32;
-    if (kbase >= a.K) break;
-    const int kr = kbase + (lane & 31);
-    const bf16_t *atr = reinterpret_cast<const bf16_t *>(a.At) + (int64_t)(kr < a.K ? kr : 0) * a.at_rs + rq;
-    f32x16 acc = zero16();
-    for (int j = 0; j < nsteps; ++j) {
-      const bf16x8 av = kr < a.K ? load8(atr + 16 * j) : zero8();
-      const bf16x8 dv = s_ok ? load8(dar + 16 * j) : zero8();
-      acc = mfma32(av, dv, acc);
-    }
-    if (!s_ok) continue;
+  bf16_t *dxr = reinterpret_cast<bf16_t *>(a.dx) + (int64_t)sc * a.dx_rs;
+  bf16x4 cur[4][4];
+#pragma unroll
+  for (int blk = 0; blk < 4; ++blk)
 #pragma unroll
     for (int g4 = 0; g4 < 4; ++g4) {
-      const int k = kbase + 8 * g4 + 4 * (lane >> 5);
+      const int k = kb0 + blk * 32 + 8 * g4 + 4 * hi;
+      cur[blk][g4] = *reinterpret_cast<const bf16x4 *>(dxr + (k < a.K ? k : a.K - 4));
+    }
+  const bf16_t *dar = reinterpret_cast<const bf16_t *>(a.da) + (int64_t)sc * a.da_rs + rq;
+  const bf16_t *atr[4];
+#pragma unroll
+  for (int blk = 0; blk < 4; ++blk) {
+    const int kr = kb0 + blk * 32 + l32;
+    atr[blk] = reinterpret_cast<const bf16_t *>(a.At) + (int64_t)(kr < a.K ? kr : a.K - 1) * a.at_rs + rq;
+  }
+  f32x16 acc[4];
+#pragma unroll
+  for (int blk = 0; blk < 4; ++blk) acc[blk] = zero16();
+  // ranks in chunks of NK steps (one chunk when the rank is at most 16 NK)
+  const int nsteps = (a.rank + 31) / 32 * 2;
+  for (int j0 = 0; j0 < nsteps; j0 += NK) {
+    bf16x8 dv[NK], av[4][NK];
+#pragma unroll
+    for (int j = 0; j < NK; ++j) dv[j] = load8(dar + 16 * (j0 + j));
+#pragma unroll
+    for (int blk = 0; blk < 4; ++blk)
+#pragma unroll
+      for (int j = 0; j < NK; ++j) av[blk][j] = load8(atr[blk] + 16 * (j0 + j));
+#pragma unroll
+    for (int blk = 0; blk < 4; ++blk)
+#pragma unroll
+      for (int j = 0; j < NK; ++j) acc[blk] = mfma32(av[blk][j], dv[j], acc[blk]);
+  }
+#pragma unroll
+  for (int blk = 0; blk < 4; ++blk) {
+    const int kbase = kb0 + blk * 32;
+    if (!s_ok || kbase >= a.K) continue;
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      const int k = kbase + 8 * g4 + 4 * hi;
       if (k >= a.K) continue;
       const uint64_t pj = ((uint64_t)s * (uint64_t)a.K + (uint64_t)k) >> 1;
       const uint32_t b0 = pair_bits(a.seed, pj), b1 = pair_bits(a.seed, pj + 1);
       const bool keep[4] = {(b0 & 0xffffu) >= a.thr, (b0 >> 16) >= a.thr, (b1 & 0xffffu) >= a.thr,
                             (b1 >> 16) >= a.thr};
-      bf16x4 cur = *reinterpret_cast<const bf16x4 *>(dxr + k);
+      bf16x4 o = cur[blk][g4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const float dh = rnd(acc[4 * g4 + e]);                      // d(dropout(x)) = T(d_a A)
+        const float dh = rnd(acc[blk][4 * g4 + e]);                 // d(dropout(x)) = T(d_a A)
         const float dl = keep[e] ? rnd(dh * a.keep_scale) : 0.f;   // dropout backward
-        cur[e] = (bf16_t)((float)cur[e] + dl);                     // + base gradient
+        o[e] = (bf16_t)((float)o[e] + dl);                         // + base gradient
       }
-      *reinterpret_cast<bf16x4 *>(dxr + k) = cur;
+      *reinterpret_cast<bf16x4 *>(dxr + k) = o;
     }
   }
 }
@@ -234,9 +439,26 @@ namespace {
 
 template <int NB>
 void launch_down_nb(const LoraDownArgs &a, hipStream_t st) {
-  const dim3 grid((unsigned)((a.S + 31) / 32)), block(kDownWaves * 64);
-  if (a.thr > 0) hipLaunchKernelGGL((lora_down_kernel<NB, true>), grid, block, 0, st, a);
-  else hipLaunchKernelGGL((lora_down_kernel<NB, false>), grid, block, 0, st, a);
+  const dim3 grid((unsigned)((a.S + 31) / 32));
+  if (a.K % 128 == 0) {
+    // enough workgroups to keep every CU's loads in flight: split K while the
+    // row blocks alone number fewer than about four per CU
+    const int nrb = (a.S + 31) / 32, nch = a.K / 128;
+    int nsplit = 1;
+    if (a.part)
+      while (nsplit < kDownMaxSplit && nrb * nsplit < 1024 && nch / (2 * nsplit) >= 2) nsplit *= 2;
+    const dim3 g2((unsigned)nrb, (unsigned)nsplit);
+    if (a.thr > 0) hipLaunchKernelGGL((lora_down_lds_kernel<NB, true>), g2, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((lora_down_lds_kernel<NB, false>), g2, dim3(256), 0, st, a);
+    if (nsplit > 1) {
+      const int64_t n = (int64_t)a.S * 32 * NB;
+      hipLaunchKernelGGL(lora_down_finish_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, a, nsplit,
+                         32 * NB);
+    }
+    return;
+  }
+  if (a.thr > 0) hipLaunchKernelGGL((lora_down_kernel<NB, true>), grid, dim3(kDownWaves * 64), 0, st, a);
+  else hipLaunchKernelGGL((lora_down_kernel<NB, false>), grid, dim3(kDownWaves * 64), 0, st, a);
 }
 
 }  // namespace
@@ -261,7 +483,13 @@ void launch_lora_down(const LoraDownArgs &a, hipStream_t st) {
 
 void launch_lora_dx(const LoraDxArgs &a, hipStream_t st) {
   const dim3 grid((unsigned)((a.K + 511) / 512), (unsigned)((a.S + 31) / 32)), block(256);
-  hipLaunchKernelGGL(lora_dx_kernel, grid, block, 0, st, a);
+  switch ((a.rank + 31) / 32) {
+    case 1: hipLaunchKernelGGL((lora_dx_kernel<2>), grid, block, 0, st, a); break;
+    case 2: hipLaunchKernelGGL((lora_dx_kernel<4>), grid, block, 0, st, a); break;
+    case 3: hipLaunchKernelGGL((lora_dx_kernel<6>), grid, block, 0, st, a); break;
+    case 4: hipLaunchKernelGGL((lora_dx_kernel<8>), grid, block, 0, st, a); break;
+    default: hipLaunchKernelGGL((lora_dx_kernel<2>), grid, block, 0, st, a); break;   // 2-step chunks
+  }
 }
 
 void launch_lora_scale_rows(const void *u, int64_t u_rs, const float *gate, float scaling, int32_t S, int32_t rank,

@@ -95,6 +95,7 @@ def test_qwen3_qkv_shape(dev, p):
     (64, 512, 384, 160, 0.1, "mixed"),      # rank above 96: chunked down-projection
     (40, 1024, 200, 64, 0.5, "mixed"),      # gate_up-like rank, heavy dropout, odd N
     (31, 128, 64, 1, 0.0, "mixed"),         # rank 1, one partial row block
+    (50, 272, 100, 24, 0.05, "mixed"),      # in_features not a multiple of 128 (direct-load kernel)
 ])
 def test_shapes(dev, S, K, N, r, p, gate):
     run_case(dev, S, K, N, r, p, gate=gate, seed=S)
