@@ -329,15 +329,112 @@ __global__ __launch_bounds__(256) void lora_down_finish_kernel(LoraDownArgs a, i
   reinterpret_cast<bf16_t *>(a.t)[(int64_t)s * a.t_rs + r] = (bf16_t)out;
 }
 
-// Grid: (ceil(K / 512), ceil(S / 32)), 4 waves; wave w covers 32 rows x 128
-// columns of dX. D^T[k][s] = sum_r A^T[k][r] d_a[s][r]; each lane holds one
+// Grid: (K / 128, ceil(S / 128)), 4 waves. The workgroup's 128 columns of
+// A^T (rank-padded rows) are copied once into LDS and shared; wave w computes
+// rows 32 w .. 32 w + 31 of the 128-row block, one 32 x 32 block at a time:
+// D[s][k] = sum_r d_a[s][r] A^T[k][r] (A operand: the lane's d_a row from
+// global memory; B operand: the A^T row of the lane's column, from LDS). The
+// rounded block T(D) goes through a per-wave LDS tile so that each lane then
+// owns 8 consecutive columns of one row: dX is read and written with 16-byte
+// accesses and each dropout hash serves its element pair. NK = 16-rank steps
+// of the padded rank (even).
+template <int NK>
+__global__ __launch_bounds__(256) void lora_dx_kernel(LoraDxArgs a) {
+  constexpr int RP = NK * 16;          // padded rank
+  constexpr int LS = RP + 8;           // LDS row stride of A^T (elements)
+  constexpr int TS = 40;               // row stride of a wave's 32 x 32 result tile (80 bytes)
+  __shared__ __attribute__((aligned(16))) bf16_t sAt[128 * LS];
+  __shared__ __attribute__((aligned(16))) bf16_t sT[4][32 * TS];
+  const int w = wave_id(), lane = threadIdx.x & 63, tid = threadIdx.x;
+  const int l32 = lane & 31, hi = lane >> 5;
+  const int kb0 = blockIdx.x * 128;
+  const int s0 = blockIdx.y * 128 + w * 32;
+  {
+    // every granule load issued before the first LDS write (one memory wait)
+    constexpr int kGran = RP / 8;      // 16-byte granules per row
+    constexpr int kPer = 128 * kGran / 256;
+    const bf16_t *src = reinterpret_cast<const bf16_t *>(a.At) + (int64_t)kb0 * a.at_rs;
+    i32x4 g16[kPer];
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int i = tid + 256 * j, r = i / kGran, g = i - r * kGran;
+      g16[j] = *reinterpret_cast<const i32x4 *>(src + (int64_t)r * a.at_rs + g * 8);
+    }
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int i = tid + 256 * j, r = i / kGran, g = i - r * kGran;
+      *reinterpret_cast<i32x4 *>(sAt + r * LS + g * 8) = g16[j];
+    }
+  }
+  const int srow = s0 + l32 < a.S ? s0 + l32 : a.S - 1;   // rows past S: computed, never stored
+  const bf16_t *dar = reinterpret_cast<const bf16_t *>(a.da) + (int64_t)srow * a.da_rs + 8 * hi;
+  bf16x8 dv[NK];
+#pragma unroll
+  for (int j = 0; j < NK; ++j) dv[j] = load8(dar + 16 * j);
+  // epilogue ownership: lane -> row er (+16 for the second half), columns ec .. ec + 7
+  const int er = lane >> 2, ec = (lane & 3) * 8;
+  bf16_t *dx = reinterpret_cast<bf16_t *>(a.dx);
+  bf16_t *tile = sT[w];
+  auto dx_at = [&](int r, int blk) {
+    const int s = s0 + r;
+    return dx + (int64_t)(s < a.S ? s : a.S - 1) * a.dx_rs + kb0 + blk * 32 + ec;
+  };
+  bf16x8 cur[2], nxt[2];
+  cur[0] = load8(dx_at(er, 0));
+  cur[1] = load8(dx_at(er + 16, 0));
+  __syncthreads();
+#pragma unroll
+  for (int blk = 0; blk < 4; ++blk) {
+    f32x16 acc = zero16();
+    const bf16_t *brow = sAt + (blk * 32 + l32) * LS + 8 * hi;
+#pragma unroll
+    for (int j = 0; j < NK; ++j) acc = mfma32(dv[j], lds_read8(brow + 16 * j), acc);
+    if (blk < 3) {
+      nxt[0] = load8(dx_at(er, blk + 1));
+      nxt[1] = load8(dx_at(er + 16, blk + 1));
+    }
+    // d(dropout(x)) = T(d_a A): lane holds column l32 of rows 8 (q / 4) + 4 hi + q % 4
+#pragma unroll
+    for (int q = 0; q < 16; ++q) tile[(8 * (q >> 2) + 4 * hi + (q & 3)) * TS + l32] = (bf16_t)acc[q];
+    __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wave's tile writes done
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int r = er + 16 * h, s = s0 + r;
+      const bf16x8 dh = lds_read8(tile + r * TS + ec);
+      if (s < a.S) {
+        const int k = kb0 + blk * 32 + ec;
+        const uint64_t pj = ((uint64_t)s * (uint64_t)a.K + (uint64_t)k) >> 1;
+        bf16x8 o = cur[h];
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+          const uint32_t bits = pair_bits(a.seed, pj + (e >> 1));
+          const bool k_lo = (bits & 0xffffu) >= a.thr, k_hi = (bits >> 16) >= a.thr;
+          const float d0 = k_lo ? rnd((float)dh[e] * a.keep_scale) : 0.f;       // dropout backward
+          const float d1 = k_hi ? rnd((float)dh[e + 1] * a.keep_scale) : 0.f;
+          o[e] = (bf16_t)((float)o[e] + d0);                                       // + base gradient
+          o[e + 1] = (bf16_t)((float)o[e + 1] + d1);
+        }
+        *reinterpret_cast<i32x4 *>(dx_at(r, blk)) = __builtin_bit_cast(i32x4, o);
+      }
+    }
+    __builtin_amdgcn_wave_barrier();   // the tile is rewritten by the next block
+    if (blk < 3) {
+      cur[0] = nxt[0];
+      cur[1] = nxt[1];
+    }
+  }
+}
+
+// General variant (any K multiple of 16, any rank). Grid: (ceil(K / 512),
+// ceil(S / 32)), 4 waves; wave w covers 32 rows x 128 columns of dX. D^T[k][s] = sum_r A^T[k][r] d_a[s][r]; each lane holds one
 // row s and four runs of four consecutive columns per 32-column block. Every
 // load (the lane's dX runs, its d_a row, the A^T rows of its four blocks) is
 // issued before the first MFMA when the rank is at most 16 NK (larger ranks
 // go in chunks of NK steps). d_a and A^T are zero-padded to a multiple of 32
 // ranks, so the step count is even.
 template <int NK>
-__global__ __launch_bounds__(256) void lora_dx_kernel(LoraDxArgs a) {
+__global__ __launch_bounds__(256) void lora_dx_rows_kernel(LoraDxArgs a) {
   const int w = wave_id(), lane = threadIdx.x & 63;
   const int l32 = lane & 31, hi = lane >> 5;
   const int s = blockIdx.y * 32 + l32;
@@ -482,13 +579,23 @@ void launch_lora_down(const LoraDownArgs &a, hipStream_t st) {
 }
 
 void launch_lora_dx(const LoraDxArgs &a, hipStream_t st) {
-  const dim3 grid((unsigned)((a.K + 511) / 512), (unsigned)((a.S + 31) / 32)), block(256);
+  if (a.K % 128 || a.rank > 128) {
+    const dim3 grid((unsigned)((a.K + 511) / 512), (unsigned)((a.S + 31) / 32)), block(256);
+    switch ((a.rank + 31) / 32) {
+      case 1: hipLaunchKernelGGL((lora_dx_rows_kernel<2>), grid, block, 0, st, a); break;
+      case 2: hipLaunchKernelGGL((lora_dx_rows_kernel<4>), grid, block, 0, st, a); break;
+      case 3: hipLaunchKernelGGL((lora_dx_rows_kernel<6>), grid, block, 0, st, a); break;
+      case 4: hipLaunchKernelGGL((lora_dx_rows_kernel<8>), grid, block, 0, st, a); break;
+      default: hipLaunchKernelGGL((lora_dx_rows_kernel<2>), grid, block, 0, st, a); break;   // 2-step chunks
+    }
+    return;
+  }
+  const dim3 grid((unsigned)(a.K / 128), (unsigned)((a.S + 127) / 128)), block(256);
   switch ((a.rank + 31) / 32) {
     case 1: hipLaunchKernelGGL((lora_dx_kernel<2>), grid, block, 0, st, a); break;
     case 2: hipLaunchKernelGGL((lora_dx_kernel<4>), grid, block, 0, st, a); break;
     case 3: hipLaunchKernelGGL((lora_dx_kernel<6>), grid, block, 0, st, a); break;
-    case 4: hipLaunchKernelGGL((lora_dx_kernel<8>), grid, block, 0, st, a); break;
-    default: hipLaunchKernelGGL((lora_dx_kernel<2>), grid, block, 0, st, a); break;   // 2-step chunks
+    default: hipLaunchKernelGGL((lora_dx_kernel<8>), grid, block, 0, st, a); break;
   }
 }
 
