@@ -166,11 +166,27 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnArgs a) {
       f32x16 sacc = zero16(), dpacc;
 #pragma unroll
       for (int r = 0; r < 16; ++r) dpacc[r] = -del;
+      // the K and V operands of k-step ks + 1 are read before the MFMAs of ks
+      // (kept in that order by the scheduling barriers)
+      auto rd = [&](const bf16_t *t, int ks) {
+        return lds_read8(reinterpret_cast<const bf16_t *>(lds_at(t, krow ^ (uint32_t)(ks << 5))));
+      };
+      bf16x8 kc = rd(tK, 0), vc = rd(tV, 0);
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        const uint32_t off = krow ^ (uint32_t)(ks << 5);
-        sacc = mfma32(lds_read8(reinterpret_cast<const bf16_t *>(lds_at(tK, off))), qf[ks], sacc);
-        dpacc = mfma32(lds_read8(reinterpret_cast<const bf16_t *>(lds_at(tV, off))), dof[ks], dpacc);
+        bf16x8 kn, vn;
+        if (ks + 1 < KS) {
+          kn = rd(tK, ks + 1);
+          vn = rd(tV, ks + 1);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        sacc = mfma32(kc, qf[ks], sacc);
+        dpacc = mfma32(vc, dof[ks], dpacc);
+        __builtin_amdgcn_sched_barrier(0);
+        if (ks + 1 < KS) {
+          kc = kn;
+          vc = vn;
+        }
       }
       if (partial) {
         // a real branch: if-converted, full tiles would pay for the masking

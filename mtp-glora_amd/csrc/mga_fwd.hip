@@ -193,15 +193,31 @@ __global__ __launch_bounds__(256, 3 - NB) void attn_fwd_kernel(AttnArgs a) {
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) sacc[kb][nb] = zero16();
+      // the K operands of k-step ks + 1 are read before the MFMAs of ks (the
+      // scheduling barriers keep that order), so each LDS read has two MFMAs
+      // of time to land instead of stalling the one that uses it
+      auto kread = [&](int ks, int kb) {
+        return lds_read8(reinterpret_cast<const bf16_t *>(lds_at(tK + kb * 32 * HD, krow ^ (uint32_t)(ks << 5))));
+      };
+      bf16x8 ka[2] = {kread(0, 0), kread(0, 1)};
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-          const bf16x8 af = lds_read8(reinterpret_cast<const bf16_t *>(
-              lds_at(tK + kb * 32 * HD, krow ^ (uint32_t)(ks << 5))));
-#pragma unroll
-          for (int nb = 0; nb < NB; ++nb) sacc[kb][nb] = mfma32(af, qf[nb][ks], sacc[kb][nb]);
+      for (int ks = 0; ks < KS; ++ks) {
+        bf16x8 kn[2];
+        if (ks + 1 < KS) {
+          kn[0] = kread(ks + 1, 0);
+          kn[1] = kread(ks + 1, 1);
         }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb) sacc[kb][nb] = mfma32(ka[kb], qf[nb][ks], sacc[kb][nb]);
+        __builtin_amdgcn_sched_barrier(0);
+        if (ks + 1 < KS) {
+          ka[0] = kn[0];
+          ka[1] = kn[1];
+        }
+      }
       bf16x8 pb[NB][4];
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) {
@@ -264,15 +280,19 @@ __global__ __launch_bounds__(256, 3 - NB) void attn_fwd_kernel(AttnArgs a) {
         }
         l_run[nb] += ps;
       }
-      // O^T += V^T P^T (each V^T operand serves the NB row blocks)
+      // O^T += V^T P^T (each V^T operand serves the NB row blocks); operand
+      // t = (16-key slice t / DB, output block t % DB), read one ahead
+      bf16x8 vcur = tro.operand(tV, 0, 0);
 #pragma unroll
-      for (int cc = 0; cc < 4; ++cc)
+      for (int t = 0; t < 4 * DB; ++t) {
+        bf16x8 vnext;
+        if (t + 1 < 4 * DB) vnext = tro.operand(tV, ((t + 1) / DB) * 16, (t + 1) % DB);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int db = 0; db < DB; ++db) {
-          const bf16x8 va = tro.operand(tV, cc * 16, db);
-#pragma unroll
-          for (int nb = 0; nb < NB; ++nb) oacc[nb][db] = mfma32(va, pb[nb][cc], oacc[nb][db]);
-        }
+        for (int nb = 0; nb < NB; ++nb) oacc[nb][t % DB] = mfma32(vcur, pb[nb][t / DB], oacc[nb][t % DB]);
+        __builtin_amdgcn_sched_barrier(0);
+        if (t + 1 < 4 * DB) vcur = vnext;
+      }
     }
 
     if (j + 1 < nstep) store_step(B ? sK0 : sK1, B ? sV0 : sV1, B ? sW0 : sW1);
