@@ -40,7 +40,9 @@ namespace {
 
 constexpr float kNegInfF = -__builtin_huge_valf();
 constexpr float kPBound = 1048576.f;   // 2^20: largest partial row sum of a step on the fast path
-constexpr int kStepKeys = 64;
+constexpr int kStepKeys = 64;                 // keys per pipeline step (a multiple of 32)
+constexpr int kStepBlocks = kStepKeys / 32;   // 32-key MFMA blocks per step
+constexpr int kStepsPerTile = kBlock / kStepKeys;
 
 typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2;
 
@@ -116,8 +118,8 @@ __global__ __launch_bounds__(256, 3 - NB) void attn_fwd_kernel(AttnArgs a) {
   const int npart = a.kv_num[qt];
   const int ntot = npart + a.fkv_num[qt];
   TileList tiles{a.kv_idx + (int64_t)qt * a.nKV, a.fkv_idx + (int64_t)qt * a.nKV, npart, ntot};
-  const int nstep = 2 * ntot;
-  auto step_base = [&](int j) { return tiles.at(j >> 1) * kBlock + (j & 1) * kStepKeys; };
+  const int nstep = kStepsPerTile * ntot;
+  auto step_base = [&](int j) { return tiles.at(j / kStepsPerTile) * kBlock + (j % kStepsPerTile) * kStepKeys; };
 
   // per-lane LDS offsets: K rows (A operand of QK^T) and the V^T transpose reads
   // K operand of k-step ks: row l32 (+ 32 kb), granule (2 ks + hi) ^ swz(l32),
@@ -182,15 +184,15 @@ __global__ __launch_bounds__(256, 3 - NB) void attn_fwd_kernel(AttnArgs a) {
     const bf16_t *tV = B ? sV1 : sV0;
     const int *tW = B ? sW1 : sW0;
     const int kbase = step_base(j);
-    const bool partial = (j >> 1) < npart;
+    const bool partial = (j / kStepsPerTile) < npart;
     if (j + 1 < nstep) load_step(j + 1, B ? sK0 : sK1, B ? sV0 : sV1);
 
     // S^T = K Q^T for 64 keys x WR queries; register r of sacc[kb][nb] is key
     // kb * 32 + 8 (r / 4) + 4 hi + r % 4 of the step, query row block nb.
     if (kbase < a.L) {
-      f32x16 sacc[2][NB];
+      f32x16 sacc[kStepBlocks][NB];
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+      for (int kb = 0; kb < kStepBlocks; ++kb)
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) sacc[kb][nb] = zero16();
       // the K operands of k-step ks + 1 are read before the MFMAs of ks (the
@@ -199,26 +201,26 @@ __global__ __launch_bounds__(256, 3 - NB) void attn_fwd_kernel(AttnArgs a) {
       auto kread = [&](int ks, int kb) {
         return lds_read8(reinterpret_cast<const bf16_t *>(lds_at(tK + kb * 32 * HD, krow ^ (uint32_t)(ks << 5))));
       };
-      bf16x8 ka[2] = {kread(0, 0), kread(0, 1)};
+      bf16x8 ka[kStepBlocks];
+#pragma unroll
+      for (int kb = 0; kb < kStepBlocks; ++kb) ka[kb] = kread(0, kb);
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        bf16x8 kn[2];
-        if (ks + 1 < KS) {
-          kn[0] = kread(ks + 1, 0);
-          kn[1] = kread(ks + 1, 1);
-        }
+        bf16x8 kn[kStepBlocks];
+        if (ks + 1 < KS)
+#pragma unroll
+          for (int kb = 0; kb < kStepBlocks; ++kb) kn[kb] = kread(ks + 1, kb);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
+        for (int kb = 0; kb < kStepBlocks; ++kb)
 #pragma unroll
           for (int nb = 0; nb < NB; ++nb) sacc[kb][nb] = mfma32(ka[kb], qf[nb][ks], sacc[kb][nb]);
         __builtin_amdgcn_sched_barrier(0);
-        if (ks + 1 < KS) {
-          ka[0] = kn[0];
-          ka[1] = kn[1];
-        }
+        if (ks + 1 < KS)
+#pragma unroll
+          for (int kb = 0; kb < kStepBlocks; ++kb) ka[kb] = kn[kb];
       }
-      bf16x8 pb[NB][4];
+      bf16x8 pb[NB][2 * kStepBlocks];
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) {
         if (partial) {
@@ -226,7 +228,7 @@ __global__ __launch_bounds__(256, 3 - NB) void attn_fwd_kernel(AttnArgs a) {
           asm volatile("");
           const int lim = qlim[nb] - kbase - 4 * hi;   // key offset (without 4 hi) must be <= lim
 #pragma unroll
-          for (int kb = 0; kb < 2; ++kb)
+          for (int kb = 0; kb < kStepBlocks; ++kb)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
               const i32x4 w4 = *reinterpret_cast<const i32x4 *>(&tW[kb * 32 + 8 * i + 4 * hi]);
@@ -242,7 +244,7 @@ __global__ __launch_bounds__(256, 3 - NB) void attn_fwd_kernel(AttnArgs a) {
         auto probs = [&](float m) {
           float ps = 0.f;
 #pragma unroll
-          for (int kb = 0; kb < 2; ++kb)
+          for (int kb = 0; kb < kStepBlocks; ++kb)
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
               i32x4 wv;
@@ -262,7 +264,7 @@ __global__ __launch_bounds__(256, 3 - NB) void attn_fwd_kernel(AttnArgs a) {
         if (__builtin_amdgcn_ballot_w64(!(ps <= kPBound))) {
           float mx = kNegInfF;
 #pragma unroll
-          for (int kb = 0; kb < 2; ++kb)
+          for (int kb = 0; kb < kStepBlocks; ++kb)
 #pragma unroll
             for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kb][nb][r]);
           mx = fmaxf(mx, xor32(mx)) * c;
@@ -284,14 +286,14 @@ __global__ __launch_bounds__(256, 3 - NB) void attn_fwd_kernel(AttnArgs a) {
       // t = (16-key slice t / DB, output block t % DB), read one ahead
       bf16x8 vcur = tro.operand(tV, 0, 0);
 #pragma unroll
-      for (int t = 0; t < 4 * DB; ++t) {
+      for (int t = 0; t < 2 * kStepBlocks * DB; ++t) {
         bf16x8 vnext;
-        if (t + 1 < 4 * DB) vnext = tro.operand(tV, ((t + 1) / DB) * 16, (t + 1) % DB);
+        if (t + 1 < 2 * kStepBlocks * DB) vnext = tro.operand(tV, ((t + 1) / DB) * 16, (t + 1) % DB);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) oacc[nb][t % DB] = mfma32(vcur, pb[nb][t / DB], oacc[nb][t % DB]);
         __builtin_amdgcn_sched_barrier(0);
-        if (t + 1 < 4 * DB) vcur = vnext;
+        if (t + 1 < 2 * kStepBlocks * DB) vcur = vnext;
       }
     }
 
