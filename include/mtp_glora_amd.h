@@ -220,7 +220,9 @@ int mga_gated_lora_fwd(const void *x, int64_t x_rs, const void *weight, int64_t 
  * :56-58): from grad_y [S, N] and the forward's x, h, t and seed,
  *   grad_B = grad_y^T t,  d_a = T(T((grad_y B) * gate) * scaling),
  *   grad_x = T(grad_y W + T(mask * T(d_a A) / (1 - p))),  grad_A = d_a^T h.
- * grad_x, grad_a, grad_b may be NULL to skip them.
+ * grad_x, grad_a, grad_b may be NULL to skip them. With dropout on, grad_x
+ * is updated in place with vector accesses: its start must be 16-byte aligned
+ * and its row stride a multiple of 4 (of 8 for the 16-byte path).
  */
 int mga_gated_lora_bwd(const void *grad_y, int64_t gy_rs, const void *x, int64_t x_rs,
                        const void *h, int64_t h_rs, const void *weight, int64_t w_rs,

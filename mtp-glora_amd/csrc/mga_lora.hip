@@ -20,7 +20,13 @@
 //   instruction; staging through LDS is what makes the first variant faster.
 // * lora_dx_kernel (dropout on): dX = T(dX + T(mask * scale * T(d_a A))) in
 //   place over the base gradient dY W: HBM-bound on dX, the rank-r product on
-//   MFMA with the output's columns along each lane's four rows; every load
+//   MFMA. A workgroup covers 128 columns x 128 rows: the A^T tile of its
+//   columns is shared through LDS, d_a goes straight into MFMA operands, and
+//   each wave transposes its rounded 32 x 32 result blocks through a small
+//   LDS tile so that a lane owns 8 consecutive columns of a row: dX moves in
+//   16-byte runs with one hash per element pair. lora_dx_rows_kernel serves
+//   K not a multiple of 128, ranks above 128 and 8-byte-aligned rows: one row
+//   per lane, the output's columns along the lane's registers, every load
 //   issued before the first MFMA.
 // * lora_scale_rows_kernel: d_a = T(T(u * gate) * s), u = dY B.
 // * lora_transpose_kernel: A^T padded to a multiple of 32 ranks (the dX
@@ -579,7 +585,8 @@ void launch_lora_down(const LoraDownArgs &a, hipStream_t st) {
 }
 
 void launch_lora_dx(const LoraDxArgs &a, hipStream_t st) {
-  if (a.K % 128 || a.rank > 128) {
+  // the LDS-staged kernel moves dX in 16-byte runs: rows must start 16-byte aligned
+  if (a.K % 128 || a.rank > 128 || a.dx_rs % 8) {
     const dim3 grid((unsigned)((a.K + 511) / 512), (unsigned)((a.S + 31) / 32)), block(256);
     switch ((a.rank + 31) / 32) {
       case 1: hipLaunchKernelGGL((lora_dx_rows_kernel<2>), grid, block, 0, st, a); break;

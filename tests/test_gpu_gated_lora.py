@@ -165,3 +165,30 @@ def test_argument_errors(dev):
         lm.gated_lora_linear(x2, W2, A2, B2, g2, 2.0)
     with pytest.raises(RuntimeError):
         lm.gated_lora_linear(x.cpu(), W.cpu(), A.cpu(), B.cpu(), None, 2.0)
+
+
+def test_dx_row_stride_multiple_of_4(dev):
+    """grad_x rows 8-byte aligned only (row stride K + 4): the in-place dropout
+    update takes its 8-byte path and still matches the oracle."""
+    lm = lora_mod()
+    lib = importlib.import_module("mtp-glora_amd._lib")
+    S, K, N, r, p, s = 96, 512, 384, 32, 0.1, 2.0
+    x, W, A, B, gt = make(S, K, N, r, dev, seed=11)
+    sd = 4242
+    y, t, h = lm.gated_lora_forward(x, W, A, B, gt, s, p, sd)
+    dy = torch.randn(S, N, generator=torch.Generator(device=dev).manual_seed(12), device=dev).bfloat16()
+    buf = torch.zeros(S, K + 4, device=dev, dtype=torch.bfloat16)
+    gx = buf[:, :K]
+    ws = lm._workspace(S, K, N, r, dev)
+    lib.call("mga_gated_lora_bwd", dy.data_ptr(), dy.stride(0), x.data_ptr(), x.stride(0), h.data_ptr(),
+             h.stride(0), W.data_ptr(), W.stride(0), A.data_ptr(), A.stride(0), B.data_ptr(), B.stride(0),
+             t.data_ptr(), t.stride(0), gt.data_ptr(), s, p, sd, S, K, N, r, gx.data_ptr(), gx.stride(0),
+             None, 0, None, 0, ws.data_ptr(), ws.numel(), torch.cuda.current_stream(dev).cuda_stream)
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(buf[:, K:]).item() == 0   # the 4 pad columns are untouched
+    X, Wn, An, Bn, G, DY = f64(x), f64(W), f64(A), f64(B), f64(gt), f64(dy)
+    keep = gl.keep_mask(sd, S, K, p)
+    dx_ref, _, _ = gl.backward(DY, X, Wn, An, Bn, G, s, keep, p)
+    d_a = s * G[:, None] * (DY @ Bn)
+    bx = U * (np.abs(dx_ref) + np.abs(DY @ Wn) + 2 / (1 - p) * (np.abs(d_a) @ np.abs(An))) + 1e-5 * np.abs(dx_ref).max()
+    check("dX (stride K + 4)", f64(gx), dx_ref, bx)
