@@ -21,12 +21,12 @@ CODE_X = -2
 def _code_mask_mod(code: torch.Tensor, P: int):
     """A mask_mod equal to the reference predicate (collator.py:323-355),
     written over the codes, so the mask stays usable by torch's flex_attention,
-    ``to_dense()`` and printing."""
-    full = torch.cat([torch.full((P,), CODE_X, dtype=code.dtype, device=code.device), code]) if P > 0 else code
+    ``to_dense()`` and printing. A cached prefix key (kv_idx < P) is a regular
+    token; nothing is computed until the mask_mod is called."""
 
     def mask_mod(b, h, q_idx, kv_idx):
         qc = code[q_idx]
-        kc = full[kv_idx]
+        kc = torch.where(kv_idx < P, CODE_X, code[(kv_idx - P).clamp(min=0)])
         return (q_idx + P >= kv_idx) & (qc != CODE_PAD) & ((kc == CODE_X) | (kc == qc))
 
     return mask_mod
@@ -61,9 +61,12 @@ class MTPBlockMask(BlockMask):
                     full_q_num_blocks=self.full_q_num_blocks, full_q_indices=self.full_q_indices)
 
     def to(self, device) -> "MTPBlockMask":
-        """Keeps the MTP metadata (``BlockMask.to`` would return a plain BlockMask)."""
+        """Keeps the MTP metadata (``BlockMask.to`` would return a plain BlockMask);
+        a mask already on ``device`` is returned as is."""
         names = ["kv_num_blocks", "kv_indices", "full_kv_num_blocks", "full_kv_indices",
                  "q_num_blocks", "q_indices", "full_q_num_blocks", "full_q_indices"]
+        if torch.device(device) == self.mtp_code.device:
+            return self
         t = {n: getattr(self, n).to(device) for n in names}
         t["code"] = self.mtp_code.to(device)
         return MTPBlockMask.from_tensors(t, self.seq_lengths[0], self.prefix_len)

@@ -6,6 +6,8 @@ error, never a reason to compute elsewhere.
 """
 from __future__ import annotations
 
+import math
+
 import torch
 
 from . import _lib
@@ -125,19 +127,19 @@ def mtp_block_mask_tensors(gate: torch.Tensor, P: int) -> dict:
     nQ = -(-S // BLOCK)
     nKV = -(-L // BLOCK)
     dev = g.device
-    i32 = dict(dtype=torch.int32, device=dev)
-    out = dict(
-        code=torch.empty(S, **i32),
-        tile_class=torch.empty(nQ * nKV, dtype=torch.int8, device=dev),
-        kv_num_blocks=torch.empty(1, 1, nQ, **i32),
-        kv_indices=torch.empty(1, 1, nQ, nKV, **i32),
-        full_kv_num_blocks=torch.empty(1, 1, nQ, **i32),
-        full_kv_indices=torch.empty(1, 1, nQ, nKV, **i32),
-        q_num_blocks=torch.empty(1, 1, nKV, **i32),
-        q_indices=torch.empty(1, 1, nKV, nQ, **i32),
-        full_q_num_blocks=torch.empty(1, 1, nKV, **i32),
-        full_q_indices=torch.empty(1, 1, nKV, nQ, **i32),
-    )
+    # one int32 allocation carved into the nine outputs (each 16-byte aligned)
+    shapes = dict(code=(S,), kv_num_blocks=(1, 1, nQ), kv_indices=(1, 1, nQ, nKV),
+                  full_kv_num_blocks=(1, 1, nQ), full_kv_indices=(1, 1, nQ, nKV),
+                  q_num_blocks=(1, 1, nKV), q_indices=(1, 1, nKV, nQ),
+                  full_q_num_blocks=(1, 1, nKV), full_q_indices=(1, 1, nKV, nQ))
+    sizes = {n: math.prod(sh) for n, sh in shapes.items()}
+    total = sum((n_ + 3) // 4 * 4 for n_ in sizes.values())
+    buf = torch.empty(total, dtype=torch.int32, device=dev)
+    out, off = {}, 0
+    for n, sh in shapes.items():
+        out[n] = buf[off:off + sizes[n]].view(sh)
+        off += (sizes[n] + 3) // 4 * 4
+    out["tile_class"] = torch.empty(nQ * nKV, dtype=torch.int8, device=dev)
     _lib.call("mga_mtp_block_mask", g.data_ptr(), g.stride(0), S, int(P),
               out["code"].data_ptr(), out["tile_class"].data_ptr(),
               out["kv_num_blocks"].data_ptr(), out["kv_indices"].data_ptr(),
