@@ -193,8 +193,10 @@ int mga_qk_norm_rope_bwd(const void *q, int64_t q_token_stride, int64_t q_head_s
 /*
  * Gated LoRA linear layer, bf16 (GatedLoRALinear.forward,
  * mtp_glora/models/layers/gated_lora.py:51-53):
- *   y = x W^T + scaling * B(A(dropout(x))) * gate
- * for x [S, K] (row stride x_rs), W [N, K], A = lora_A.weight [rank, K],
+ *   y = x W^T + scaling * B(A(dropout(x))) * gate,
+ * computed as y = T(x W^T + T(t B^T)) (the base GEMM accumulates onto the
+ * rounded LoRA term), for x [S, K] (row stride x_rs), W [N, K], A =
+ * lora_A.weight [rank, K],
  * B = lora_B.weight [N, rank], gate [S] fp32 (NULL = 1; the reference's
  * clamped gate mask). Writes y [S, N] and, for the backward, t [S, rpad]
  * (rpad = rank rounded up to 32; t = T(T(scaling * T(h A^T)) * gate), T =

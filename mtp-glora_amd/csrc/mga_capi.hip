@@ -356,8 +356,6 @@ int mga_gated_lora_fwd(const void *x, int64_t x_rs, const void *weight, int64_t 
     return fail(MGA_ERR_INVALID, "%s: workspace of %lld bytes needed", fn, (long long)lora_ws_bytes(S, K, rank));
   const LoraWs w = lora_ws(workspace, S, K, rank);
   hipStream_t st = (hipStream_t)stream;
-  // y = x W^T
-  if ((rc = blas(fn, false, true, S, N, K, x, x_rs, weight, w_rs, false, y, y_rs, w, st)) != MGA_OK) return rc;
   // t = T(T(s T(dropout(x) A^T)) gate)
   mga::LoraDownArgs a = {};
   a.x = x; a.x_rs = x_rs; a.A = lora_a; a.a_rs = a_rs; a.gate = gate; a.scaling = scaling;
@@ -365,8 +363,10 @@ int mga_gated_lora_fwd(const void *x, int64_t x_rs, const void *weight, int64_t 
   a.t = t; a.t_rs = t_rs; a.part = w.part; a.S = S; a.K = K; a.rank = rank;
   mga::launch_lora_down(a, st);
   if ((rc = check_launch(fn)) != MGA_OK) return rc;
-  // y += t B^T
-  if ((rc = blas(fn, false, true, S, N, rank, t, t_rs, lora_b, b_rs, true, y, y_rs, w, st)) != MGA_OK) return rc;
+  // y = T(t B^T), then y = T(x W^T + y): the base GEMM reads the LoRA term in
+  // its epilogue (free in a compute-bound GEMM) instead of a second pass over y
+  if ((rc = blas(fn, false, true, S, N, rank, t, t_rs, lora_b, b_rs, false, y, y_rs, w, st)) != MGA_OK) return rc;
+  if ((rc = blas(fn, false, true, S, N, K, x, x_rs, weight, w_rs, true, y, y_rs, w, st)) != MGA_OK) return rc;
   return MGA_OK;
 }
 
@@ -407,9 +407,8 @@ int mga_gated_lora_bwd(const void *grad_y, int64_t gy_rs, const void *x, int64_t
   if (grad_b && (rc = blas(fn, true, false, N, rank, S, grad_y, gy_rs, t, t_rs, false, grad_b, gb_rs, w, st)))
     return rc;
   if (grad_x) {
-    // dX = dY W, then the LoRA path through dropout
-    if ((rc = blas(fn, false, false, S, K, N, grad_y, gy_rs, weight, w_rs, false, grad_x, gx_rs, w, st)) != MGA_OK)
-      return rc;
+    // the LoRA path's gradient first (through dropout when it is on), then
+    // dX = T(dY W + that): the base GEMM accumulates onto it in its epilogue
     if (thr) {
       mga::launch_lora_transpose(lora_a, a_rs, rank, K, (int32_t)rp, w.at, rp, st);
       mga::LoraDxArgs d = {};
@@ -417,9 +416,11 @@ int mga_gated_lora_bwd(const void *grad_y, int64_t gy_rs, const void *x, int64_t
       d.keep_scale = keep_scale(dropout_p); d.thr = thr; d.seed = seed; d.S = S; d.K = K; d.rank = rank;
       mga::launch_lora_dx(d, st);
       if ((rc = check_launch(fn)) != MGA_OK) return rc;
-    } else if ((rc = blas(fn, false, false, S, K, rank, w.da, rp, lora_a, a_rs, true, grad_x, gx_rs, w, st))) {
+    } else if ((rc = blas(fn, false, false, S, K, rank, w.da, rp, lora_a, a_rs, false, grad_x, gx_rs, w, st))) {
       return rc;
     }
+    if ((rc = blas(fn, false, false, S, K, N, grad_y, gy_rs, weight, w_rs, true, grad_x, gx_rs, w, st)) != MGA_OK)
+      return rc;
   }
   // dA = d_a^T dropout(x)
   if (grad_a && (rc = blas(fn, true, false, rank, K, S, w.da, rp, thr ? h : x, thr ? h_rs : x_rs, false, grad_a,

@@ -18,16 +18,18 @@
 //   reads its operands straight from global memory, K split over 8 waves.
 //   Operand loads that give each lane its own row touch 32 cache lines per
 //   instruction; staging through LDS is what makes the first variant faster.
-// * lora_dx_kernel (dropout on): dX = T(dX + T(mask * scale * T(d_a A))) in
-//   place over the base gradient dY W: HBM-bound on dX, the rank-r product on
-//   MFMA. A workgroup covers 128 columns x 128 rows: the A^T tile of its
-//   columns is shared through LDS, d_a goes straight into MFMA operands, and
-//   each wave transposes its rounded 32 x 32 result blocks through a small
-//   LDS tile so that a lane owns 8 consecutive columns of a row: dX moves in
-//   16-byte runs with one hash per element pair. lora_dx_rows_kernel serves
-//   K not a multiple of 128, ranks above 128 and 8-byte-aligned rows: one row
-//   per lane, the output's columns along the lane's registers, every load
-//   issued before the first MFMA.
+// * lora_dx_kernel (dropout on): the LoRA path's input gradient
+//   L = T(mask * T(scale * T(d_a A))), written to dX; the base gradient dY W
+//   is then accumulated on top by hipBLASLt (beta = 1), so dX is written once
+//   here and read once inside that compute-bound GEMM. The rank-r product
+//   runs on MFMA. A workgroup covers 128 columns x 128 rows: the A^T tile of
+//   its columns is shared through LDS, d_a goes straight into MFMA operands,
+//   and each wave transposes its rounded 32 x 32 result blocks through a
+//   small LDS tile so that a lane owns 8 consecutive columns of a row: dX is
+//   written in 16-byte runs with one hash per element pair.
+//   lora_dx_rows_kernel serves K not a multiple of 128, ranks above 128 and
+//   8-byte-aligned rows: one row per lane, the output's columns along the
+//   lane's registers.
 // * lora_scale_rows_kernel: d_a = T(T(u * gate) * s), u = dY B.
 // * lora_transpose_kernel: A^T padded to a multiple of 32 ranks (the dX
 //   kernel's MFMA operand wants rank-contiguous rows).
@@ -341,9 +343,9 @@ __global__ __launch_bounds__(256) void lora_down_finish_kernel(LoraDownArgs a, i
 // D[s][k] = sum_r d_a[s][r] A^T[k][r] (A operand: the lane's d_a row from
 // global memory; B operand: the A^T row of the lane's column, from LDS). The
 // rounded block T(D) goes through a per-wave LDS tile so that each lane then
-// owns 8 consecutive columns of one row: dX is read and written with 16-byte
-// accesses and each dropout hash serves its element pair. NK = 16-rank steps
-// of the padded rank (even).
+// owns 8 consecutive columns of one row: dX is written with 16-byte stores
+// and each dropout hash serves its element pair. NK = 16-rank steps of the
+// padded rank (even).
 template <int NK>
 __global__ __launch_bounds__(256) void lora_dx_kernel(LoraDxArgs a) {
   constexpr int RP = NK * 16;          // padded rank
@@ -385,9 +387,6 @@ __global__ __launch_bounds__(256) void lora_dx_kernel(LoraDxArgs a) {
     const int s = s0 + r;
     return dx + (int64_t)(s < a.S ? s : a.S - 1) * a.dx_rs + kb0 + blk * 32 + ec;
   };
-  bf16x8 cur[2], nxt[2];
-  cur[0] = load8(dx_at(er, 0));
-  cur[1] = load8(dx_at(er + 16, 0));
   __syncthreads();
 #pragma unroll
   for (int blk = 0; blk < 4; ++blk) {
@@ -395,10 +394,6 @@ __global__ __launch_bounds__(256) void lora_dx_kernel(LoraDxArgs a) {
     const bf16_t *brow = sAt + (blk * 32 + l32) * LS + 8 * hi;
 #pragma unroll
     for (int j = 0; j < NK; ++j) acc = mfma32(dv[j], lds_read8(brow + 16 * j), acc);
-    if (blk < 3) {
-      nxt[0] = load8(dx_at(er, blk + 1));
-      nxt[1] = load8(dx_at(er + 16, blk + 1));
-    }
     // d(dropout(x)) = T(d_a A): lane holds column l32 of rows 8 (q / 4) + 4 hi + q % 4
 #pragma unroll
     for (int q = 0; q < 16; ++q) tile[(8 * (q >> 2) + 4 * hi + (q & 3)) * TS + l32] = (bf16_t)acc[q];
@@ -411,33 +406,27 @@ __global__ __launch_bounds__(256) void lora_dx_kernel(LoraDxArgs a) {
       if (s < a.S) {
         const int k = kb0 + blk * 32 + ec;
         const uint64_t pj = ((uint64_t)s * (uint64_t)a.K + (uint64_t)k) >> 1;
-        bf16x8 o = cur[h];
+        bf16x8 o;
 #pragma unroll
         for (int e = 0; e < 8; e += 2) {
           const uint32_t bits = pair_bits(a.seed, pj + (e >> 1));
           const bool k_lo = (bits & 0xffffu) >= a.thr, k_hi = (bits >> 16) >= a.thr;
-          const float d0 = k_lo ? rnd((float)dh[e] * a.keep_scale) : 0.f;       // dropout backward
-          const float d1 = k_hi ? rnd((float)dh[e + 1] * a.keep_scale) : 0.f;
-          o[e] = (bf16_t)((float)o[e] + d0);                                       // + base gradient
-          o[e + 1] = (bf16_t)((float)o[e + 1] + d1);
+          o[e] = (bf16_t)(k_lo ? (float)dh[e] * a.keep_scale : 0.f);           // dropout backward
+          o[e + 1] = (bf16_t)(k_hi ? (float)dh[e + 1] * a.keep_scale : 0.f);
         }
         *reinterpret_cast<i32x4 *>(dx_at(r, blk)) = __builtin_bit_cast(i32x4, o);
       }
     }
     __builtin_amdgcn_wave_barrier();   // the tile is rewritten by the next block
-    if (blk < 3) {
-      cur[0] = nxt[0];
-      cur[1] = nxt[1];
-    }
   }
 }
 
 // General variant (any K multiple of 16, any rank). Grid: (ceil(K / 512),
 // ceil(S / 32)), 4 waves; wave w covers 32 rows x 128 columns of dX. D^T[k][s] = sum_r A^T[k][r] d_a[s][r]; each lane holds one
 // row s and four runs of four consecutive columns per 32-column block. Every
-// load (the lane's dX runs, its d_a row, the A^T rows of its four blocks) is
-// issued before the first MFMA when the rank is at most 16 NK (larger ranks
-// go in chunks of NK steps). d_a and A^T are zero-padded to a multiple of 32
+// load (its d_a row, the A^T rows of its four blocks) is issued before the
+// first MFMA when the rank is at most 16 NK (larger ranks go in chunks of NK
+// steps). d_a and A^T are zero-padded to a multiple of 32
 // ranks, so the step count is even.
 template <int NK>
 __global__ __launch_bounds__(256) void lora_dx_rows_kernel(LoraDxArgs a) {
@@ -449,14 +438,6 @@ __global__ __launch_bounds__(256) void lora_dx_rows_kernel(LoraDxArgs a) {
   const int rq = 8 * hi;
   const int kb0 = blockIdx.x * 512 + w * 128;
   bf16_t *dxr = reinterpret_cast<bf16_t *>(a.dx) + (int64_t)sc * a.dx_rs;
-  bf16x4 cur[4][4];
-#pragma unroll
-  for (int blk = 0; blk < 4; ++blk)
-#pragma unroll
-    for (int g4 = 0; g4 < 4; ++g4) {
-      const int k = kb0 + blk * 32 + 8 * g4 + 4 * hi;
-      cur[blk][g4] = *reinterpret_cast<const bf16x4 *>(dxr + (k < a.K ? k : a.K - 4));
-    }
   const bf16_t *dar = reinterpret_cast<const bf16_t *>(a.da) + (int64_t)sc * a.da_rs + rq;
   const bf16_t *atr[4];
 #pragma unroll
@@ -494,12 +475,11 @@ __global__ __launch_bounds__(256) void lora_dx_rows_kernel(LoraDxArgs a) {
       const uint32_t b0 = pair_bits(a.seed, pj), b1 = pair_bits(a.seed, pj + 1);
       const bool keep[4] = {(b0 & 0xffffu) >= a.thr, (b0 >> 16) >= a.thr, (b1 & 0xffffu) >= a.thr,
                             (b1 >> 16) >= a.thr};
-      bf16x4 o = cur[blk][g4];
+      bf16x4 o;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const float dh = rnd(acc[blk][4 * g4 + e]);                 // d(dropout(x)) = T(d_a A)
-        const float dl = keep[e] ? rnd(dh * a.keep_scale) : 0.f;   // dropout backward
-        o[e] = (bf16_t)((float)o[e] + dl);                         // + base gradient
+        o[e] = (bf16_t)(keep[e] ? dh * a.keep_scale : 0.f);         // dropout backward
       }
       *reinterpret_cast<bf16x4 *>(dxr + k) = o;
     }

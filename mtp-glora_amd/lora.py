@@ -7,9 +7,9 @@ unchanged), same initialisation, and ``forward(x, gate_mask)`` returning
 
     base_layer(x) + lora_scaling * lora_B(lora_A(dropout(x))) * gate_mask
 
-in one call of ``mga_gated_lora_fwd`` (hipBLASLt for the base GEMM and the
-rank-r up-projection accumulated into the output, a HIP kernel for the
-down-projection with dropout fused in); the backward is one call of
+in one call of ``mga_gated_lora_fwd`` (a HIP kernel for the down-projection
+with dropout fused in, hipBLASLt for the rank-r up-projection and the base
+GEMM accumulated onto it); the backward is one call of
 ``mga_gated_lora_bwd``. ``apply_lora_to_model`` mirrors the reference's
 function of the same name (:61-100): it wraps the matching ``nn.Linear``
 children (rank and alpha x3 for ``qkv_proj``, x2 for ``gate_up_proj``) and
@@ -20,8 +20,9 @@ the dropout mask comes from a counter hash of a per-call seed (drawn from
 torch's default generator) rather than torch's dropout generator; the scaling
 and gate are applied to the rank-r activations before lora_B rather than to
 lora_B's output (the same value when the scaling is a power of two and the
-gate is 0 / 1, as in the reference's configurations), and that up-projection
-is accumulated into the base output in fp32 before one rounding. bf16 only,
+gate is 0 / 1, as in the reference's configurations), and the base product
+is accumulated in fp32 onto the rounded LoRA term before one final rounding
+(in the backward likewise for dX). bf16 only,
 no biases (Qwen3 and Llama projections have none), base weights frozen.
 """
 from __future__ import annotations

@@ -4,11 +4,12 @@ same bf16 inputs, the mask included.
 
 Tolerances follow the bf16 roundings on each path (u = 2^-8 covers two
 roundings of 2^-9):
-* y: the base product is rounded, then the rank-r term (whose activations t
-  are rounded) is added and the sum rounded:
+* y: the rank-r term (whose activations t are rounded) is rounded, the base
+  product accumulated onto it and the sum rounded:
   |y - y*| <= u (|y*| + |x W^T| + s g |h A^T| |B|^T) + 1e-5 max|y*|;
-* dX: the base gradient dY W is rounded, the LoRA term goes through three
-  roundings (u = dY B, d_a A, the dropout scaling) and the sum is rounded:
+* dX: the LoRA term goes through three roundings (u = dY B, d_a A, the
+  dropout scaling), the base gradient dY W is accumulated onto it and the sum
+  is rounded:
   |dX - dX*| <= u (|dX*| + |dY W| + 2 |d_a| |A| / (1 - p)) + 1e-5 max|dX*|;
 * dA = d_a^T h and dB = dY^T t (sums over the S rows of rounded factors):
   |d - d*| <= u (|d*| + |a|^T |b|) with |a|^T |b| the sum of absolute products;
