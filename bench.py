@@ -275,7 +275,7 @@ def gated_lora_phase(torch, timer, S: int, K: int, N: int, rank: int, p: float, 
     # HIP kernels' algorithmic bytes: the down-projection reads x and writes
     # the dropout output (+ t); the dX update reads and writes dX
     down_bytes = S * K * 2 * (2 if p > 0 else 1) + S * ((rank + 31) // 32 * 32) * 2
-    dx_bytes = 2 * S * K * 2 if p > 0 else 0
+    dx_bytes = S * K * 2 if p > 0 else 0          # the LoRA term of dX, written once
     return {"S": S, "in": K, "out": N, "rank": rank, "dropout": p, "dtype": "bf16",
             "fwd_ms": round(t_f, 4), "bwd_ms": round(t_b, 4), "base_gemm_ms": round(t_gemm, 4),
             "fwd_tflops": round(fl_fwd / (t_f * 1e-3) / 1e12, 1), "bwd_tflops": round(fl_bwd / (t_b * 1e-3) / 1e12, 1),
