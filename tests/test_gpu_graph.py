@@ -1,0 +1,75 @@
+"""The hot path inside one captured HIP graph: block-mask build, K/V staging
+append, attention forward, both backward passes and the regular-row commit
+(the tensor-level calls a training step makes, no host sync inside) are
+captured once and replayed. Every kernel is deterministic (fixed-order
+reductions, no atomics) and nothing in the path clears memory with
+hipMemsetAsync, so each replay must reproduce the eager results bit for bit,
+with eager work and synchronisations between the replays."""
+import pytest
+import torch
+
+from gpu_helpers import chunk_layout, qkv
+
+pytestmark = pytest.mark.gpu
+
+
+def test_attention_step_graph_replays_bit_exact(mga, dev):
+    ops = mga.ops
+    n_reg, n_anchor, draft, P, Hq, Hkv, D = 300, 25, 4, 200, 8, 2, 128
+    print(f"case n_reg={n_reg} P={P} Hq={Hq} Hkv={Hkv} D={D}", flush=True)
+    seq = chunk_layout(n_reg, n_anchor, draft, P, seed=3, pad=11)
+    S = len(seq.gate)
+    L = P + S
+    gate = torch.tensor(seq.gate, device=dev)[None]
+    reg = torch.tensor(seq.regular, device=dev)
+    q, k, v, kp, vp, do = qkv(S, P, Hq, Hkv, D, torch.bfloat16, dev, seed=5)
+    kbuf = torch.zeros(Hkv, L + 64, D, dtype=torch.bfloat16, device=dev)
+    vbuf = torch.zeros_like(kbuf)
+    kbuf[:, :P] = kp[0]
+    vbuf[:, :P] = vp[0]
+    committed_k = torch.zeros(Hkv, S + 16, D, dtype=torch.bfloat16, device=dev)
+    committed_v = torch.zeros_like(committed_k)
+    idx, cnt = ops.regular_index(reg)
+    torch.cuda.synchronize()
+    R = int(cnt.item())
+    scale = D ** -0.5
+
+    def work():
+        t = ops.mtp_block_mask_tensors(gate, P)
+        bm = {n: t[n] for n in ("kv_num_blocks", "kv_indices", "full_kv_num_blocks", "full_kv_indices",
+                                "q_num_blocks", "q_indices", "full_q_num_blocks", "full_q_indices")}
+        ops.kv_append(k, v, kbuf, vbuf, dst_offset=P)
+        kf, vf = kbuf[None, :, :L], vbuf[None, :, :L]
+        o, lse = ops.attn_fwd(q, kf, vf, t["code"], bm, P, scale)
+        dq, dk, dv = ops.attn_bwd(q, kf, vf, o, lse, do, t["code"], bm, P, scale, P)
+        ops.kv_append(k, v, committed_k, committed_v, dst_offset=0, idx=idx, n_rows=R)
+        return [t["code"], *bm.values(), o, lse, dq, dk, dv, committed_k[:, :R], committed_v[:, :R]]
+
+    eager = [x.clone() for x in work()]
+    torch.cuda.synchronize()
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        work()   # warm-up on a side stream before capture, as torch requires
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = work()
+
+    for rep in range(3):
+        # eager work between replays: scribble over the outputs and the cache rows
+        for x in out:
+            if x.dtype.is_floating_point:
+                x.fill_(float("nan"))
+            else:
+                x.fill_(-7)
+        kbuf[:, P:].fill_(3.0)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for i, (got, want) in enumerate(zip(out, eager)):
+            assert torch.equal(got, want), f"replay {rep}: output {i} differs from the eager run"
+        print(f"  replay {rep}: {len(out)} outputs bit-exact", flush=True)
