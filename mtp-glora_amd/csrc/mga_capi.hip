@@ -271,14 +271,16 @@ int64_t lora_rpad(int32_t rank) { return (rank + 31) / 32 * 32; }
 struct LoraWs {
   void *blas, *u, *da, *at;
   float *part;
+  void *packed;
 };
 
 // [hipBLASLt workspace | u = dY B : S x rpad | d_a : S x rpad | A^T : K x rpad
-//  (bf16) | split-K partial sums of the down-projection: 8 x S x 96 fp32]
+//  (bf16) | split-K partial sums of the down-projection: 8 x S x 96 fp32 |
+//  lora_A in MFMA-operand order, up to 96 ranks at a time: K / 16 x 3 KB]
 int64_t lora_ws_bytes(int32_t S, int32_t K, int32_t rank) {
   const int64_t rp = lora_rpad(rank);
   return kBlasWorkspace + 2 * align256((int64_t)S * rp * 2) + align256((int64_t)K * rp * 2) +
-         align256((int64_t)8 * S * 96 * 4);
+         align256((int64_t)8 * S * 96 * 4) + align256((int64_t)K / 16 * 3 * 1024);
 }
 
 LoraWs lora_ws(void *ws, int32_t S, int32_t K, int32_t rank) {
@@ -290,6 +292,7 @@ LoraWs lora_ws(void *ws, int32_t S, int32_t K, int32_t rank) {
   w.da = static_cast<char *>(w.u) + align256((int64_t)S * rp * 2);
   w.at = static_cast<char *>(w.da) + align256((int64_t)S * rp * 2);
   w.part = reinterpret_cast<float *>(static_cast<char *>(w.at) + align256((int64_t)K * rp * 2));
+  w.packed = reinterpret_cast<char *>(w.part) + align256((int64_t)8 * S * 96 * 4);
   return w;
 }
 
@@ -360,7 +363,7 @@ int mga_gated_lora_fwd(const void *x, int64_t x_rs, const void *weight, int64_t 
   mga::LoraDownArgs a = {};
   a.x = x; a.x_rs = x_rs; a.A = lora_a; a.a_rs = a_rs; a.gate = gate; a.scaling = scaling;
   a.keep_scale = keep_scale(dropout_p); a.thr = thr; a.seed = seed; a.h = thr ? h : nullptr; a.h_rs = h_rs;
-  a.t = t; a.t_rs = t_rs; a.part = w.part; a.S = S; a.K = K; a.rank = rank;
+  a.t = t; a.t_rs = t_rs; a.part = w.part; a.packed = w.packed; a.S = S; a.K = K; a.rank = rank;
   mga::launch_lora_down(a, st);
   if ((rc = check_launch(fn)) != MGA_OK) return rc;
   // y = T(t B^T), then y = T(x W^T + y): the base GEMM reads the LoRA term in

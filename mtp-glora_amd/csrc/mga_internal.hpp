@@ -84,6 +84,7 @@ struct LoraDownArgs {
   void *h; int64_t h_rs;               // dropout output [S, K] (thr > 0)
   void *t; int64_t t_rs;               // [S, rpad] bf16 out
   float *part;                         // split-K partial sums: 8 x S x 96 fp32, or null (no split)
+  void *packed;                        // lora_A in MFMA-operand order: K / 16 x 3 blocks of 1 KB
   int32_t S, K, rank;
 };
 struct LoraDxArgs {

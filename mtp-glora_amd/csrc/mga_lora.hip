@@ -11,13 +11,16 @@
 //   dropout(x) drawn on the fly (and written out when dropout is on: the
 //   backward's dA GEMM reads it, as the reference keeps its dropout output).
 //   HBM-bound on x; v_mfma_f32_32x32x16_bf16 with 32 rows per workgroup.
-//   lora_down_lds_kernel (K a multiple of 128) copies 128-wide chunks of the
-//   x rows and of A into LDS with direct loads (1 KB per instruction) and
-//   splits K over up to 8 workgroups per row block, whose fp32 partial sums
-//   lora_down_finish_kernel adds in a fixed order; lora_down_kernel (other K)
-//   reads its operands straight from global memory, K split over 8 waves.
-//   Operand loads that give each lane its own row touch 32 cache lines per
-//   instruction; staging through LDS is what makes the first variant faster.
+//   lora_down_ring_kernel (K a multiple of 128) streams 128-wide chunks of
+//   the x rows through a ring of four LDS buffers with direct loads (1 KB per
+//   instruction, three chunks ahead) and reads A's operands from a copy in
+//   MFMA-operand order (lora_pack_a_kernel: one contiguous 1 KB read per
+//   operand); it splits K over up to 8 workgroups per row block, whose fp32
+//   partial sums lora_down_finish_kernel adds in a fixed order.
+//   lora_down_kernel (other K) reads its operands straight from global
+//   memory, K split over 8 waves. Operand loads that give each lane its own
+//   row touch 32 cache lines per instruction; staging x through LDS and
+//   packing A is what makes the first kernel faster.
 // * lora_dx_kernel (dropout on): the LoRA path's input gradient
 //   L = T(mask * T(scale * T(d_a A))), written to dX; the base gradient dY W
 //   is then accumulated on top by hipBLASLt (beta = 1), so dX is written once
@@ -76,6 +79,10 @@ __device__ __forceinline__ bf16x8 zero8() {
   for (int i = 0; i < 8; ++i) z[i] = (bf16_t)0.f;
   return z;
 }
+
+// s_waitcnt immediate waiting for vmcnt <= n only (gfx9 encoding: vmcnt[3:0]
+// in bits 3:0, vmcnt[5:4] in bits 15:14; expcnt and lgkmcnt at their maxima)
+constexpr int vmcnt_imm(int n) { return (n & 0xf) | (0x7 << 4) | (0xf << 8) | ((n >> 4) << 14); }
 
 constexpr int kDownWaves = 8;
 constexpr int kDownMaxSplit = 8;   // split-K parts of the LDS down-projection (partials: 8 x S x 96 fp32)
@@ -195,17 +202,44 @@ __global__ __launch_bounds__(kDownWaves * 64) void lora_down_kernel(LoraDownArgs
   }
 }
 
-// LDS-staged variant for K a multiple of 128. Grid: ceil(S / 32) workgroups
-// of 4 waves; chunks of 128 k of the 32 x rows and of the 32 NB rows of A are
-// copied global -> LDS by direct loads (1 KB per instruction, swizzled rows),
-// double-buffered in named buffers; wave w takes k steps 2w, 2w + 1 of each
-// chunk, its MFMA operands read from LDS. The waves' partial sums are reduced
-// in a fixed order through the (then idle) A buffers.
-template <int NB, bool DROP>
-__global__ __launch_bounds__(256) void lora_down_lds_kernel(LoraDownArgs a) {
-  constexpr int HD = 128, NRA = 32 * NB;
-  __shared__ __attribute__((aligned(16))) bf16_t sX0[32 * HD], sX1[32 * HD];
-  __shared__ __attribute__((aligned(16))) bf16_t sA0[NRA * HD], sA1[NRA * HD];
+// lora_A in MFMA-operand order: 1 KB block (kstep, nb) = K/16 k-steps x NB
+// rank blocks, lane (l32, hi) holding A[32 nb + l32][16 kstep + 8 hi .. + 8]
+// (zero past the rank), so every operand load of the down-projection below is
+// one contiguous 1 KB wave read. One thread per 16-byte granule.
+__global__ __launch_bounds__(256) void lora_pack_a_kernel(const bf16_t *A, int64_t a_rs, int32_t rank, int32_t K,
+                                                          int32_t nb_n, i32x4 *pk) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)(K / 16) * nb_n * 64) return;
+  const int lane = (int)(i & 63);
+  const int64_t blk = i >> 6;
+  const int nb = (int)(blk % nb_n);
+  const int64_t kstep = blk / nb_n;
+  const int r = nb * 32 + (lane & 31);
+  const int64_t k = kstep * 16 + 8 * (lane >> 5);
+  i32x4 v = {0, 0, 0, 0};
+  if (r < rank) v = *reinterpret_cast<const i32x4 *>(A + (int64_t)r * a_rs + k);
+  pk[i] = v;
+}
+
+// Down-projection for K a multiple of 128 with the x rows streamed through a
+// ring of four LDS buffers (direct loads, three 128-column chunks ahead) and
+// lora_A's operands read straight from the packed copy (L2-resident, one 1 KB
+// read per operand). Grid (ceil(S / 32), nsplit): a workgroup of 4 waves owns
+// 32 rows and a contiguous share of the chunks; wave w takes k-steps 2w, 2w+1
+// of every chunk, and the waves' sums are added in a fixed order at the end.
+// Every wave issues the same memory instructions in every iteration (a chunk
+// past the share reloads the share's last chunk into its free buffer; the
+// operand loads of a chunk past the share read the last one), so the waits
+// can name exact counts: the chunk's own loads, and its operands. vmcnt
+// retires loads in issue order but stores out of order with them, so when
+// the kernel also writes the dropout output it waits for everything instead.
+template <int NB, bool DROP, bool WRITE_H>
+__global__ __launch_bounds__(256) void lora_down_ring_kernel(LoraDownArgs a) {
+  constexpr int HD = 128, NRA = 32 * NB, RING = 4, TILE = 32 * HD;
+  // per-iteration vector-memory loads of a wave after its chunk loads: the
+  // next chunk's operands (2 NB)
+  constexpr int kOps = 2 * NB;
+  __shared__ __attribute__((aligned(16))) bf16_t sX[RING * TILE];
   const int w = wave_id(), lane = threadIdx.x & 63;
   const int l32 = lane & 31, hi = lane >> 5;
   const int s0 = blockIdx.x * 32;
@@ -213,41 +247,58 @@ __global__ __launch_bounds__(256) void lora_down_lds_kernel(LoraDownArgs a) {
   const bool row_ok = row < a.S;
   const int nrows = a.S - s0 < 32 ? a.S - s0 : 32;
   const bf16_t *xb = reinterpret_cast<const bf16_t *>(a.x) + (int64_t)s0 * a.x_rs;
-  const bf16_t *ab = reinterpret_cast<const bf16_t *>(a.A);
+  const i32x4 *pk = reinterpret_cast<const i32x4 *>(a.packed);
   DmaLane<HD, 32> dx;
-  DmaLane<HD, NRA> da;
   dx.init();
-  da.init();
-  const uint32_t lrx = dx.lane_row(a.x_rs), lra = da.lane_row(a.a_rs);
-  // operand of k step ks: row l32 (+ 32 nb), granule (2 ks + hi) ^ swz(l32)
+  const uint32_t lrx = dx.lane_row(a.x_rs);
   const uint32_t orow = opaque_u32((uint32_t)(l32 * HD + (((uint32_t)hi ^ swz<HD>(l32)) << 3)) * 2u);
-  bf16_t *hr = (DROP && a.h) ? reinterpret_cast<bf16_t *>(a.h) + (int64_t)(row_ok ? row : 0) * a.h_rs : nullptr;
+  bf16_t *hr = WRITE_H ? reinterpret_cast<bf16_t *>(a.h) + (int64_t)(row_ok ? row : 0) * a.h_rs : nullptr;
   const uint64_t prow = (uint64_t)(row_ok ? row : 0) * (uint64_t)a.K;
-  // this workgroup's share of the K chunks (split K: gridDim.y parts)
   const int nall = a.K / HD;
   const int cbeg = (int)((int64_t)nall * blockIdx.y / gridDim.y);
   const int nchunks = (int)((int64_t)nall * (blockIdx.y + 1) / gridDim.y) - cbeg;
 
-  auto issue = [&](int c, bf16_t *tx, bf16_t *ta) {
-    const int col = (cbeg + c) * HD;
+  auto issue = [&](int c) {   // chunk c of the share into buffer c % RING (past the share: its last chunk)
+    const int col = (cbeg + min(c, nchunks - 1)) * HD;
+    bf16_t *tx = sX + (c % RING) * TILE;
     if (nrows == 32) dx.issue(tx, xb + col, a.x_rs, lrx);
     else dx.issue_clamped(tx, xb + col, a.x_rs, nrows);
-    if (a.rank == NRA) da.issue(ta, ab + col, a.a_rs, lra);
-    else da.issue_clamped(ta, ab + col, a.a_rs, a.rank);
   };
+  auto load_ops = [&](int c, bf16x8 (&op)[2][NB]) {
+    const int64_t kstep0 = (int64_t)(cbeg + min(c, nchunks - 1)) * (HD / 16) + 2 * w;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+        op[j][nb] = __builtin_bit_cast(bf16x8, pk[((kstep0 + j) * NB + nb) * 64 + lane]);
+  };
+
   f32x16 acc[NB];
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) acc[nb] = zero16();
-
-  auto step = [&](auto bsel, int c) {
-    constexpr int Bf = decltype(bsel)::value;
-    const bf16_t *tx = Bf ? sX1 : sX0;
-    const bf16_t *ta = Bf ? sA1 : sA0;
-    if (c + 1 < nchunks) issue(c + 1, Bf ? sX0 : sX1, Bf ? sA0 : sA1);
+  // operands of the current / next chunk in two named register sets that
+  // swap roles each iteration (the loop runs two chunks per trip)
+  bf16x8 opa[2][NB], opb[2][NB];
+  auto chunk = [&](int c, bf16x8 (&opc)[2][NB], bf16x8 (&opn)[2][NB]) {
+    // this wave's loads of chunk c have landed (the first iterations wait for
+    // everything). vmcnt counts in issue order only while no store is in
+    // flight, so with the dropout output written here the wait is a full one.
+    if (c >= RING - 1 && !WRITE_H) __builtin_amdgcn_s_waitcnt(vmcnt_imm(3 * kOps + 4));
+    else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    // every wave's part of chunk c is in; chunk c - 1's buffer is free. A bare
+    // barrier between compiler fences: __syncthreads' memory fence would make
+    // the compiler wait for every load in flight, the ring's included.
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    issue(c + RING - 1);
+    // the operands of chunk c (issued before the two loads just above)
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(2));
+    const uint32_t ob = orow + (uint32_t)((c % RING) * TILE * 2);
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int ks = 2 * w + j;
-      bf16x8 xv = lds_read8(reinterpret_cast<const bf16_t *>(lds_at(tx, orow ^ (uint32_t)(ks << 5))));
+      bf16x8 xv = lds_read8(reinterpret_cast<const bf16_t *>(lds_at(sX, ob ^ (uint32_t)(ks << 5))));
       if constexpr (DROP) {
         const int k0 = (cbeg + c) * HD + ks * 16 + 8 * hi;
         const uint64_t pj = (prow + (uint64_t)k0) >> 1;
@@ -258,46 +309,45 @@ __global__ __launch_bounds__(256) void lora_down_lds_kernel(LoraDownArgs a) {
           xv[e] = k_lo ? (bf16_t)((float)xv[e] * a.keep_scale) : (bf16_t)0.f;
           xv[e + 1] = k_hi ? (bf16_t)((float)xv[e + 1] * a.keep_scale) : (bf16_t)0.f;
         }
-        if (row_ok && hr) *reinterpret_cast<i32x4 *>(hr + k0) = __builtin_bit_cast(i32x4, xv);
+        // one store instruction per k-step (lanes of rows past S masked off;
+        // a wave always has a row below S, so the store is never skipped)
+        if constexpr (WRITE_H)
+          if (row_ok) *reinterpret_cast<i32x4 *>(hr + k0) = __builtin_bit_cast(i32x4, xv);
       }
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb) {
-        const bf16x8 av =
-            lds_read8(reinterpret_cast<const bf16_t *>(lds_at(ta + nb * 32 * HD, orow ^ (uint32_t)(ks << 5))));
-        acc[nb] = mfma32(xv, av, acc[nb]);
-      }
+      for (int nb = 0; nb < NB; ++nb) acc[nb] = mfma32(xv, opc[j][nb], acc[nb]);
     }
-    if (c + 1 < nchunks) __builtin_amdgcn_s_waitcnt(0);   // this thread's loads of the next chunk landed
-    __syncthreads();
+    load_ops(c + 1, opn);
   };
 
-  if (nchunks > 0) issue(0, sX0, sA0);
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
+  issue(0);
+  issue(1);
+  issue(2);
+  load_ops(0, opa);
   for (int c = 0; c < nchunks; c += 2) {
-    step(std::integral_constant<int, 0>{}, c);
-    if (c + 1 < nchunks) step(std::integral_constant<int, 1>{}, c + 1);
+    chunk(c, opa, opb);
+    if (c + 1 < nchunks) chunk(c + 1, opb, opa);
   }
-
-  // fixed-order reduction: waves 1..3 park their sums in the A buffers, wave 0 adds
-  float *p1 = reinterpret_cast<float *>(sA0), *p2 = reinterpret_cast<float *>(sA0) + NB * 1024;
-  float *p3 = reinterpret_cast<float *>(sA1);
-  if (w > 0) {
-    float *mine = w == 1 ? p1 : (w == 2 ? p2 : p3);
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-      for (int q = 0; q < 16; ++q) mine[(nb * 16 + q) * 64 + lane] = acc[nb][q];
-  }
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));   // the ring's trailing loads
   __syncthreads();
+
+  // fixed-order reduction through the ring, one rank block at a time
+  float *park = reinterpret_cast<float *>(sX);
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    if (w > 0)
+#pragma unroll
+      for (int q = 0; q < 16; ++q) park[((w - 1) * 16 + q) * 64 + lane] = acc[nb][q];
+    __syncthreads();
+    if (w == 0)
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        const int o = q * 64 + lane;
+        acc[nb][q] += park[o] + park[16 * 64 + o] + park[32 * 64 + o];
+      }
+    __syncthreads();
+  }
   if (w != 0) return;
-#pragma unroll
-  for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-    for (int q = 0; q < 16; ++q) {
-      const int o = (nb * 16 + q) * 64 + lane;
-      acc[nb][q] += p1[o] + p2[o] + p3[o];
-    }
   if (gridDim.y > 1) {   // fp32 partial sums [split][S][32 NB]; lora_down_finish_kernel adds them
     float *part = a.part + (int64_t)blockIdx.y * a.S * NRA;
 #pragma unroll
@@ -523,16 +573,21 @@ namespace {
 template <int NB>
 void launch_down_nb(const LoraDownArgs &a, hipStream_t st) {
   const dim3 grid((unsigned)((a.S + 31) / 32));
-  if (a.K % 128 == 0) {
-    // enough workgroups to keep every CU's loads in flight: split K while the
-    // row blocks alone number fewer than about four per CU
+  if (a.K % 128 == 0 && a.packed) {
+    // lora_A into operand order, then the ring kernel; split K until every CU
+    // has about two workgroups, each keeping at least four chunks
+    const int64_t ng = (int64_t)(a.K / 16) * NB * 64;
+    hipLaunchKernelGGL(lora_pack_a_kernel, dim3((unsigned)((ng + 255) / 256)), dim3(256), 0, st,
+                       reinterpret_cast<const bf16_t *>(a.A), a.a_rs, a.rank, a.K, NB,
+                       reinterpret_cast<i32x4 *>(a.packed));
     const int nrb = (a.S + 31) / 32, nch = a.K / 128;
     int nsplit = 1;
     if (a.part)
-      while (nsplit < kDownMaxSplit && nrb * nsplit < 1024 && nch / (2 * nsplit) >= 2) nsplit *= 2;
+      while (nsplit < kDownMaxSplit && nrb * nsplit < 512 && nch / (2 * nsplit) >= 4) nsplit *= 2;
     const dim3 g2((unsigned)nrb, (unsigned)nsplit);
-    if (a.thr > 0) hipLaunchKernelGGL((lora_down_lds_kernel<NB, true>), g2, dim3(256), 0, st, a);
-    else hipLaunchKernelGGL((lora_down_lds_kernel<NB, false>), g2, dim3(256), 0, st, a);
+    if (a.thr > 0 && a.h) hipLaunchKernelGGL((lora_down_ring_kernel<NB, true, true>), g2, dim3(256), 0, st, a);
+    else if (a.thr > 0) hipLaunchKernelGGL((lora_down_ring_kernel<NB, true, false>), g2, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((lora_down_ring_kernel<NB, false, false>), g2, dim3(256), 0, st, a);
     if (nsplit > 1) {
       const int64_t n = (int64_t)a.S * 32 * NB;
       hipLaunchKernelGGL(lora_down_finish_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, a, nsplit,
