@@ -10,7 +10,7 @@
   Each kernel's figure is its last dispatch in the pass (the hot-path launch;
   set-up work such as the prefix fill runs before it).
 
-    python mtp-glora_amd/rocprof_summary.py stats gpurun_out/prof/bench_kernel_stats.csv
+    python mtp-glora_amd/rocprof_summary.py stats TRACE_DIR/bench_kernel_stats.csv
     python mtp-glora_amd/rocprof_summary.py traffic --fetch F.csv --write W.csv \\
         --calib-read BYTES --calib-write BYTES --config 2 -o profiles/config2_traffic.json
 """
