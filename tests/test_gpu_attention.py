@@ -63,6 +63,8 @@ SMALL = [
     dict(n_reg=256, n_anchor=16, draft=4, P=128, Hq=4, Hkv=2, D=64),            # config-1 head_dim
     dict(n_reg=180, n_anchor=20, draft=4, P=96, Hq=2, Hkv=2, D=64, tail=True, pad=20),  # MHA
     dict(n_reg=60, n_anchor=5, draft=2, P=0, Hq=4, Hkv=2, D=128, pad=3),        # S < 128
+    dict(n_reg=200, n_anchor=20, draft=4, P=130, Hq=8, Hkv=1, D=128),           # G = 8: two head slices
+    dict(n_reg=220, n_anchor=30, draft=3, P=70, Hq=8, Hkv=2, D=64, pad=9),      # G = 4 at head_dim 64
 ]
 
 
