@@ -200,7 +200,9 @@ int mga_qk_norm_rope_bwd(const void *q, int64_t q_token_stride, int64_t q_head_s
  * B = lora_B.weight [N, rank], gate [S] fp32 (NULL = 1; the reference's
  * clamped gate mask). Writes y [S, N] and, for the backward, t [S, rpad]
  * (rpad = rank rounded up to 32; t = T(T(scaling * T(h A^T)) * gate), T =
- * bf16 rounding, h = dropout(x)) and, when dropout_p > 0, h [S, K].
+ * bf16 rounding, h = dropout(x)) and, when dropout_p > 0 and h is not
+ * NULL, h [S, K] (NULL: h is not kept and the backward draws the mask again
+ * from x, which needs K a multiple of 128).
  * Dropout keeps element i of the flattened [S, K] input by a hash of
  * (seed, i) with probability 1 - round(65536 p) / 65536 and scales kept
  * elements by 1 / (1 - p). K must be a multiple of 16; x, lora_A and h are read
@@ -222,9 +224,11 @@ int mga_gated_lora_fwd(const void *x, int64_t x_rs, const void *weight, int64_t 
  * :56-58): from grad_y [S, N] and the forward's x, h, t and seed,
  *   grad_B = grad_y^T t,  d_a = T(T((grad_y B) * gate) * scaling),
  *   grad_x = T(grad_y W + T(mask * T(d_a A) / (1 - p))),  grad_A = d_a^T h.
- * grad_x, grad_a, grad_b may be NULL to skip them. With dropout on, grad_x
- * is updated in place with vector accesses: its start must be 16-byte aligned
- * and its row stride a multiple of 4 (of 8 for the 16-byte path).
+ * grad_x, grad_a, grad_b may be NULL to skip them; h may be NULL when the
+ * forward kept no dropout output (grad_A then recomputes it from x and the
+ * seed; K a multiple of 128). With dropout on, grad_x is written with
+ * vector accesses: its start must be 16-byte aligned and its row stride a
+ * multiple of 4 (of 8 for the 16-byte path).
  */
 int mga_gated_lora_bwd(const void *grad_y, int64_t gy_rs, const void *x, int64_t x_rs,
                        const void *h, int64_t h_rs, const void *weight, int64_t w_rs,

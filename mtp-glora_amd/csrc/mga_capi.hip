@@ -272,15 +272,18 @@ struct LoraWs {
   void *blas, *u, *da, *at;
   float *part;
   void *packed;
+  float *dapart;
 };
 
 // [hipBLASLt workspace | u = dY B : S x rpad | d_a : S x rpad | A^T : K x rpad
 //  (bf16) | split-K partial sums of the down-projection: 8 x S x 96 fp32 |
-//  lora_A in MFMA-operand order, up to 96 ranks at a time: K / 16 x 3 KB]
+//  lora_A in MFMA-operand order, up to 96 ranks at a time: K / 16 x 3 KB |
+//  split partial sums of grad_A: 16 x rpad x K fp32]
 int64_t lora_ws_bytes(int32_t S, int32_t K, int32_t rank) {
   const int64_t rp = lora_rpad(rank);
   return kBlasWorkspace + 2 * align256((int64_t)S * rp * 2) + align256((int64_t)K * rp * 2) +
-         align256((int64_t)8 * S * 96 * 4) + align256((int64_t)K / 16 * 3 * 1024);
+         align256((int64_t)8 * S * 96 * 4) + align256((int64_t)K / 16 * 3 * 1024) +
+         align256((int64_t)mga::kDaMaxSplit * rp * K * 4);
 }
 
 LoraWs lora_ws(void *ws, int32_t S, int32_t K, int32_t rank) {
@@ -293,6 +296,7 @@ LoraWs lora_ws(void *ws, int32_t S, int32_t K, int32_t rank) {
   w.at = static_cast<char *>(w.da) + align256((int64_t)S * rp * 2);
   w.part = reinterpret_cast<float *>(static_cast<char *>(w.at) + align256((int64_t)K * rp * 2));
   w.packed = reinterpret_cast<char *>(w.part) + align256((int64_t)8 * S * 96 * 4);
+  w.dapart = reinterpret_cast<float *>(static_cast<char *>(w.packed) + align256((int64_t)K / 16 * 3 * 1024));
   return w;
 }
 
@@ -354,7 +358,7 @@ int mga_gated_lora_fwd(const void *x, int64_t x_rs, const void *weight, int64_t 
       (rc = check_vec_rows(fn, "lora_A", lora_a, a_rs, K)) || (rc = check_rows_ld(fn, "lora_B", lora_b, b_rs, rank)) ||
       (rc = check_rows_ld(fn, "output", y, y_rs, N)) || (rc = check_rows_ld(fn, "t", t, t_rs, rp)))
     return rc;
-  if (thr > 0 && (rc = check_vec_rows(fn, "dropout output h", h, h_rs, K)) != MGA_OK) return rc;
+  if (thr > 0 && h && (rc = check_vec_rows(fn, "dropout output h", h, h_rs, K)) != MGA_OK) return rc;
   if (!workspace || workspace_bytes < lora_ws_bytes(S, K, rank))
     return fail(MGA_ERR_INVALID, "%s: workspace of %lld bytes needed", fn, (long long)lora_ws_bytes(S, K, rank));
   const LoraWs w = lora_ws(workspace, S, K, rank);
@@ -362,7 +366,7 @@ int mga_gated_lora_fwd(const void *x, int64_t x_rs, const void *weight, int64_t 
   // t = T(T(s T(dropout(x) A^T)) gate)
   mga::LoraDownArgs a = {};
   a.x = x; a.x_rs = x_rs; a.A = lora_a; a.a_rs = a_rs; a.gate = gate; a.scaling = scaling;
-  a.keep_scale = keep_scale(dropout_p); a.thr = thr; a.seed = seed; a.h = thr ? h : nullptr; a.h_rs = h_rs;
+  a.keep_scale = keep_scale(dropout_p); a.thr = thr; a.seed = seed; a.h = thr && h ? h : nullptr; a.h_rs = h_rs;
   a.t = t; a.t_rs = t_rs; a.part = w.part; a.packed = w.packed; a.S = S; a.K = K; a.rank = rank;
   mga::launch_lora_down(a, st);
   if ((rc = check_launch(fn)) != MGA_OK) return rc;
@@ -393,9 +397,17 @@ int mga_gated_lora_bwd(const void *grad_y, int64_t gy_rs, const void *x, int64_t
     return rc;
   if (grad_x && thr && (!aligned16(grad_x) || gx_rs % 4))
     return fail(MGA_ERR_INVALID, "%s: grad_x must be 16-byte aligned with a row stride multiple of 4", fn);
-  if (grad_a && ((rc = check_rows_ld(fn, "grad_A", grad_a, ga_rs, K)) ||
-                 (rc = check_rows_ld(fn, thr ? "dropout output h" : "x", thr ? h : x, thr ? h_rs : x_rs, K))))
+  // with dropout and no saved dropout output, grad_A draws the mask again from x
+  const bool da_from_x = grad_a && thr && !h;
+  if (grad_a && (rc = check_rows_ld(fn, "grad_A", grad_a, ga_rs, K))) return rc;
+  if (da_from_x) {
+    if (K % 128)
+      return fail(MGA_ERR_INVALID, "%s: the dropout output h is needed when in_features (%d) is not a multiple of 128",
+                  fn, K);
+    if ((rc = check_vec_rows(fn, "x", x, x_rs, K))) return rc;
+  } else if (grad_a && (rc = check_rows_ld(fn, thr ? "dropout output h" : "x", thr ? h : x, thr ? h_rs : x_rs, K))) {
     return rc;
+  }
   if (grad_b && (rc = check_rows_ld(fn, "grad_B", grad_b, gb_rs, rank))) return rc;
   if (!workspace || workspace_bytes < lora_ws_bytes(S, K, rank))
     return fail(MGA_ERR_INVALID, "%s: workspace of %lld bytes needed", fn, (long long)lora_ws_bytes(S, K, rank));
@@ -426,9 +438,16 @@ int mga_gated_lora_bwd(const void *grad_y, int64_t gy_rs, const void *x, int64_t
       return rc;
   }
   // dA = d_a^T dropout(x)
-  if (grad_a && (rc = blas(fn, true, false, rank, K, S, w.da, rp, thr ? h : x, thr ? h_rs : x_rs, false, grad_a,
-                           ga_rs, w, st)))
+  if (da_from_x) {
+    mga::LoraDaArgs d = {};
+    d.x = x; d.x_rs = x_rs; d.da = w.da; d.da_rs = rp; d.dA = grad_a; d.dA_rs = ga_rs; d.part = w.dapart;
+    d.keep_scale = keep_scale(dropout_p); d.thr = thr; d.seed = seed; d.S = S; d.K = K; d.rank = rank;
+    mga::launch_lora_da(d, st);
+    if ((rc = check_launch(fn)) != MGA_OK) return rc;
+  } else if (grad_a && (rc = blas(fn, true, false, rank, K, S, w.da, rp, thr ? h : x, thr ? h_rs : x_rs, false,
+                                  grad_a, ga_rs, w, st))) {
     return rc;
+  }
   return MGA_OK;
 }
 

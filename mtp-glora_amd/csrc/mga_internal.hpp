@@ -96,7 +96,19 @@ struct LoraDxArgs {
   uint64_t seed;
   int32_t S, K, rank;
 };
+struct LoraDaArgs {
+  const void *x; int64_t x_rs;         // [S, K] bf16, the layer input
+  const void *da; int64_t da_rs;       // [S, rpad] bf16 gradient at lora_A's output (zero past the rank)
+  void *dA; int64_t dA_rs;             // [rank, K] bf16 out
+  float *part;                         // split partial sums [nsplit, 32 ceil(rank / 32), K] fp32
+  float keep_scale;
+  uint32_t thr;                        // 16-bit drop threshold (> 0)
+  uint64_t seed;
+  int32_t S, K, rank;
+};
+constexpr int kDaMaxSplit = 16;
 void launch_lora_down(const LoraDownArgs &a, hipStream_t stream);
+void launch_lora_da(const LoraDaArgs &a, hipStream_t stream);
 void launch_lora_dx(const LoraDxArgs &a, hipStream_t stream);
 void launch_lora_scale_rows(const void *u, int64_t u_rs, const float *gate, float scaling, int32_t S,
                             int32_t rank, int32_t rpad, void *da, int64_t da_rs, hipStream_t stream);

@@ -8,8 +8,8 @@
 // kernels here fuse what a library GEMM cannot:
 //
 // * the down-projection t = T(T(s * T(h A^T)) * gate) for every row, h =
-//   dropout(x) drawn on the fly (and written out when dropout is on: the
-//   backward's dA GEMM reads it, as the reference keeps its dropout output).
+//   dropout(x) drawn on the fly (written out only on request: the backward's
+//   lora_da_kernel draws the same mask again from x).
 //   HBM-bound on x; v_mfma_f32_32x32x16_bf16 with 32 rows per workgroup.
 //   lora_down_ring_kernel (K a multiple of 128) streams 128-wide chunks of
 //   the x rows through a ring of four LDS buffers with direct loads (1 KB per
@@ -536,6 +536,126 @@ __global__ __launch_bounds__(256) void lora_dx_rows_kernel(LoraDxArgs a) {
   }
 }
 
+// grad_A = d_a^T dropout(x) with the dropout drawn again from x (so the
+// forward need not keep its dropout output): K a multiple of 128, ranks in
+// launches of up to 128. Grid (K / 128, nsplit): a workgroup owns 128
+// columns and a share of the rows, 32 at a time. Each step stages the rows'
+// dropout(x) (one hash per element pair, as in the forward) and their d_a
+// through registers into LDS (double-buffered), and wave w accumulates
+// D[r][k] = sum_s d_a[s][r] h[s][k] for its 32 columns and every rank block,
+// both MFMA operands read with the transposed LDS read (lane = r or k,
+// 8 consecutive rows s). Split partial sums go to fp32 [split][r][k] and
+// lora_da_finish_kernel adds them in a fixed order.
+template <int NB>
+__global__ __launch_bounds__(256) void lora_da_kernel(LoraDaArgs a, int r0) {
+  constexpr int HD = 128, TILE = 32 * HD;
+  __shared__ __attribute__((aligned(16))) bf16_t sX0[TILE], sX1[TILE], sD0[TILE], sD1[TILE];
+  const int w = wave_id(), tid = threadIdx.x, lane = tid & 63;
+  const int l32 = lane & 31, hi = lane >> 5;
+  const int kc0 = blockIdx.x * HD;
+  const int nst = (a.S + 31) / 32;
+  const int st0 = (int)((int64_t)nst * blockIdx.y / gridDim.y);
+  const int st1 = (int)((int64_t)nst * (blockIdx.y + 1) / gridDim.y);
+  const int rc = min(a.rank - r0, 32 * NB);   // ranks of this launch
+  const bf16_t *xb = reinterpret_cast<const bf16_t *>(a.x);
+  const bf16_t *db = reinterpret_cast<const bf16_t *>(a.da) + r0;
+  TrOffsets<HD> tro;
+  tro.init(lane);
+  // staged granules of one step: x 2 per thread, d_a NB / 2 per thread (rounded up)
+  constexpr int kDG = (32 * NB * 4 + 255) / 256;
+  i32x4 gx[2], gd[kDG];
+  auto load = [&](int st) {
+    const int s0 = st * 32;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int gi = tid + 256 * i, r = gi >> 4, g = gi & 15;
+      const int s = s0 + r;
+      const i32x4 v = *reinterpret_cast<const i32x4 *>(xb + (int64_t)min(s, a.S - 1) * a.x_rs + kc0 + 8 * g);
+      bf16x8 h = __builtin_bit_cast(bf16x8, v);
+      const uint64_t pj = ((uint64_t)min(s, a.S - 1) * (uint64_t)a.K + (uint64_t)(kc0 + 8 * g)) >> 1;
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        const uint32_t bits = pair_bits(a.seed, pj + (e >> 1));
+        const bool k_lo = s < a.S && (bits & 0xffffu) >= a.thr, k_hi = s < a.S && (bits >> 16) >= a.thr;
+        h[e] = k_lo ? (bf16_t)((float)h[e] * a.keep_scale) : (bf16_t)0.f;
+        h[e + 1] = k_hi ? (bf16_t)((float)h[e + 1] * a.keep_scale) : (bf16_t)0.f;
+      }
+      gx[i] = __builtin_bit_cast(i32x4, h);
+    }
+#pragma unroll
+    for (int i = 0; i < kDG; ++i) {
+      const int gi = tid + 256 * i, r = gi / (4 * NB), g = gi % (4 * NB);
+      const int s = s0 + r;
+      i32x4 v = {0, 0, 0, 0};
+      if (gi < 32 * 4 * NB && s < a.S) v = *reinterpret_cast<const i32x4 *>(db + (int64_t)s * a.da_rs + 8 * g);
+      gd[i] = v;
+    }
+  };
+  auto store = [&](bf16_t *tx, bf16_t *td) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int gi = tid + 256 * i;
+      *reinterpret_cast<i32x4 *>(tx + tile_off<HD>(gi >> 4, gi & 15)) = gx[i];
+    }
+#pragma unroll
+    for (int i = 0; i < kDG; ++i) {
+      const int gi = tid + 256 * i;
+      if (gi < 32 * 4 * NB) *reinterpret_cast<i32x4 *>(td + tile_off<HD>(gi / (4 * NB), gi % (4 * NB))) = gd[i];
+    }
+  };
+  f32x16 acc[NB];
+#pragma unroll
+  for (int rb = 0; rb < NB; ++rb) acc[rb] = zero16();
+  auto step = [&](auto bsel, int st) {
+    constexpr int B = decltype(bsel)::value;
+    const bf16_t *tx = B ? sX1 : sX0;
+    const bf16_t *td = B ? sD1 : sD0;
+    if (st + 1 < st1) load(st + 1);
+#pragma unroll
+    for (int ss = 0; ss < 2; ++ss) {
+      const bf16x8 hb = tro.operand(tx, 16 * ss, w);
+#pragma unroll
+      for (int rb = 0; rb < NB; ++rb) acc[rb] = mfma32(tro.operand(td, 16 * ss, rb), hb, acc[rb]);
+    }
+    if (st + 1 < st1) store(B ? sX0 : sX1, B ? sD0 : sD1);
+    __syncthreads();
+  };
+  if (st0 < st1) {
+    load(st0);
+    store(sX0, sD0);
+  }
+  __syncthreads();
+  for (int st = st0; st < st1; st += 2) {
+    step(std::integral_constant<int, 0>{}, st);
+    if (st + 1 < st1) step(std::integral_constant<int, 1>{}, st + 1);
+  }
+  // lane holds column kc0 + 32 w + l32 of rows 8 (q / 4) + 4 hi + q % 4 of each rank block
+  const int k = kc0 + 32 * w + l32;
+  const int rp = (a.rank + 31) / 32 * 32;
+#pragma unroll
+  for (int rb = 0; rb < NB; ++rb)
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      const int r = 32 * rb + 8 * (q >> 2) + 4 * hi + (q & 3);
+      if (r >= rc) continue;
+      if (gridDim.y > 1)
+        a.part[((int64_t)blockIdx.y * rp + r0 + r) * a.K + k] = acc[rb][q];
+      else
+        reinterpret_cast<bf16_t *>(a.dA)[(int64_t)(r0 + r) * a.dA_rs + k] = (bf16_t)acc[rb][q];
+    }
+}
+
+// grad_A[r][k] = T(sum over the splits, in order) of lora_da_kernel's partials.
+__global__ __launch_bounds__(256) void lora_da_finish_kernel(LoraDaArgs a, int nsplit) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)a.rank * a.K) return;
+  const int r = (int)(i / a.K), k = (int)(i - (int64_t)r * a.K);
+  const int rp = (a.rank + 31) / 32 * 32;
+  float v = 0.f;
+  for (int y = 0; y < nsplit; ++y) v += a.part[((int64_t)y * rp + r) * a.K + k];
+  reinterpret_cast<bf16_t *>(a.dA)[(int64_t)r * a.dA_rs + k] = (bf16_t)v;
+}
+
 // d_a[s][r] = T(T(u[s][r] * gate[s]) * s) for r < rank, 0 up to rpad.
 __global__ __launch_bounds__(256) void lora_scale_rows_kernel(const bf16_t *u, int64_t u_rs, const float *gate,
                                                               float scaling, int32_t S, int32_t rank, int32_t rpad,
@@ -638,6 +758,25 @@ void launch_lora_dx(const LoraDxArgs &a, hipStream_t st) {
     case 2: hipLaunchKernelGGL((lora_dx_kernel<4>), grid, block, 0, st, a); break;
     case 3: hipLaunchKernelGGL((lora_dx_kernel<6>), grid, block, 0, st, a); break;
     default: hipLaunchKernelGGL((lora_dx_kernel<8>), grid, block, 0, st, a); break;
+  }
+}
+
+void launch_lora_da(const LoraDaArgs &a, hipStream_t st) {
+  const int nkb = a.K / 128, nst = (a.S + 31) / 32;
+  int nsplit = 1;
+  while (nsplit < kDaMaxSplit && nkb * nsplit < 512 && nst / (2 * nsplit) >= 4) nsplit *= 2;
+  const dim3 grid((unsigned)nkb, (unsigned)nsplit), block(256);
+  for (int r0 = 0; r0 < a.rank; r0 += 128) {
+    switch ((min(a.rank - r0, 128) + 31) / 32) {
+      case 1: hipLaunchKernelGGL((lora_da_kernel<1>), grid, block, 0, st, a, r0); break;
+      case 2: hipLaunchKernelGGL((lora_da_kernel<2>), grid, block, 0, st, a, r0); break;
+      case 3: hipLaunchKernelGGL((lora_da_kernel<3>), grid, block, 0, st, a, r0); break;
+      default: hipLaunchKernelGGL((lora_da_kernel<4>), grid, block, 0, st, a, r0); break;
+    }
+  }
+  if (nsplit > 1) {
+    const int64_t n = (int64_t)a.rank * a.K;
+    hipLaunchKernelGGL(lora_da_finish_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, a, nsplit);
   }
 }
 

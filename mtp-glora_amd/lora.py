@@ -69,14 +69,17 @@ def _workspace(S: int, K: int, N: int, rank: int, device) -> torch.Tensor:
     return torch.empty(n, dtype=torch.uint8, device=device)
 
 
-def gated_lora_forward(x2, weight, lora_a, lora_b, gate, scaling: float, p: float, seed: int):
-    """y [S, N], t [S, rpad] and (p > 0) h [S, K] for x2 [S, K]."""
+def gated_lora_forward(x2, weight, lora_a, lora_b, gate, scaling: float, p: float, seed: int,
+                       keep_h: bool = False):
+    """y [S, N], t [S, rpad] and h [S, K] = dropout(x2) for x2 [S, K]. h is
+    None unless dropout is on and either ``keep_h`` asks for it or K is not a
+    multiple of 128 (the backward otherwise draws the mask again from x2)."""
     S, K = x2.shape
     N, rank = weight.shape[0], lora_a.shape[0]
     dev = x2.device
     y = torch.empty(S, N, device=dev, dtype=torch.bfloat16)
     t = torch.empty(S, _rpad(rank), device=dev, dtype=torch.bfloat16)
-    h = torch.empty(S, K, device=dev, dtype=torch.bfloat16) if p > 0 else None
+    h = torch.empty(S, K, device=dev, dtype=torch.bfloat16) if p > 0 and (keep_h or K % 128) else None
     ws = _workspace(S, K, N, rank, dev)
     _lib.call("mga_gated_lora_fwd", x2.data_ptr(), x2.stride(0), weight.data_ptr(), weight.stride(0),
               lora_a.data_ptr(), lora_a.stride(0), lora_b.data_ptr(), lora_b.stride(0),

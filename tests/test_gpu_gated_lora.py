@@ -56,18 +56,27 @@ def check(name, got, ref, bound):
 
 
 def run_case(dev, S, K, N, r, p, gate="mixed", seed=0, scaling=2.0):
+    """The layer's own path (no dropout output kept when K is a multiple of
+    128: grad_A draws the mask again from x), checked against the oracle; with
+    dropout on, also the path that keeps h: h bit for bit, the same y, and a
+    grad_A from hipBLASLt over h that meets the same bound."""
     lm = lora_mod()
     x, W, A, B, gt = make(S, K, N, r, dev, seed, gate)
     sd = 1234567 + seed
     y, t, h = lm.gated_lora_forward(x, W, A, B, gt, scaling, p, sd)
+    assert h is None or K % 128 or p == 0
     dy = torch.randn(S, N, generator=torch.Generator(device=dev).manual_seed(seed + 7), device=dev).bfloat16()
     gx, ga, gb = lm.gated_lora_backward(dy, x, h, t, W, A, B, gt, scaling, p, sd, True, True, True)
+    if p > 0:
+        yk, tk, hk = lm.gated_lora_forward(x, W, A, B, gt, scaling, p, sd, keep_h=True)
+        _, gak, _ = lm.gated_lora_backward(dy, x, hk, tk, W, A, B, gt, scaling, p, sd, False, True, False)
     torch.cuda.synchronize()
     X, Wn, An, Bn, G, DY = f64(x), f64(W), f64(A), f64(B), f64(gt), f64(dy)
     keep = gl.keep_mask(sd, S, K, p) if p > 0 else None
-    if p > 0:   # the kernel's dropout output, bit for bit
+    if p > 0:   # the kernel's dropout output, bit for bit, and the same forward with or without it
         want = (keep * f64(x.float().mul(1.0 / (1.0 - p)).bfloat16()))
-        np.testing.assert_array_equal(f64(h), want)
+        np.testing.assert_array_equal(f64(hk), want)
+        assert torch.equal(yk, y) and torch.equal(tk, t)
     Gv = np.ones(S) if G is None else G
     H = X if keep is None else X * keep / (1 - p)
     ks = 1.0 if p == 0 else 1.0 / (1 - p)
@@ -79,6 +88,8 @@ def run_case(dev, S, K, N, r, p, gate="mixed", seed=0, scaling=2.0):
     bx = U * (np.abs(dx_ref) + np.abs(DY @ Wn) + 2 * ks * (np.abs(d_a) @ np.abs(An))) + 1e-5 * np.abs(dx_ref).max()
     check("dX", f64(gx), dx_ref, bx)
     check("dA", f64(ga), dA_ref, U * (np.abs(dA_ref) + np.abs(d_a).T @ np.abs(H)) + 1e-30)
+    if p > 0:
+        check("dA (kept h)", f64(gak), dA_ref, U * (np.abs(dA_ref) + np.abs(d_a).T @ np.abs(H)) + 1e-30)
     T = scaling * Gv[:, None] * (H @ An.T)
     check("dB", f64(gb), dB_ref, U * (np.abs(dB_ref) + np.abs(DY).T @ np.abs(T)) + 1e-30)
     return y, t, h
@@ -107,7 +118,7 @@ def test_full_qkv_forward_against_fp32(dev):
     lm = lora_mod()
     S, K, N, r, p, s = 5120, 4096, 6144, 96, 0.05, 2.0
     x, W, A, B, gt = make(S, K, N, r, dev, seed=3)
-    y, t, h = lm.gated_lora_forward(x, W, A, B, gt, s, p, 99)
+    y, t, h = lm.gated_lora_forward(x, W, A, B, gt, s, p, 99, keep_h=True)
     hf, xf, Wf, Af, Bf = h.float(), x.float(), W.float(), A.float(), B.float()
     base = xf @ Wf.T
     lora = s * gt[:, None] * ((hf @ Af.T) @ Bf.T)
@@ -181,8 +192,8 @@ def test_dx_row_stride_multiple_of_4(dev):
     buf = torch.zeros(S, K + 4, device=dev, dtype=torch.bfloat16)
     gx = buf[:, :K]
     ws = lm._workspace(S, K, N, r, dev)
-    lib.call("mga_gated_lora_bwd", dy.data_ptr(), dy.stride(0), x.data_ptr(), x.stride(0), h.data_ptr(),
-             h.stride(0), W.data_ptr(), W.stride(0), A.data_ptr(), A.stride(0), B.data_ptr(), B.stride(0),
+    lib.call("mga_gated_lora_bwd", dy.data_ptr(), dy.stride(0), x.data_ptr(), x.stride(0), None,
+             0, W.data_ptr(), W.stride(0), A.data_ptr(), A.stride(0), B.data_ptr(), B.stride(0),
              t.data_ptr(), t.stride(0), gt.data_ptr(), s, p, sd, S, K, N, r, gx.data_ptr(), gx.stride(0),
              None, 0, None, 0, ws.data_ptr(), ws.numel(), torch.cuda.current_stream(dev).cuda_stream)
     torch.cuda.synchronize()
