@@ -272,17 +272,20 @@ def gated_lora_phase(torch, timer, S: int, K: int, N: int, rank: int, p: float, 
         out.backward(dyc)
         secs.append(time.perf_counter() - t0)
     cpu_s = sorted(secs[1:])[0]
-    # HIP kernels' algorithmic bytes: the down-projection reads x and writes
-    # the dropout output (+ t); the dX update reads and writes dX
-    down_bytes = S * K * 2 * (2 if p > 0 else 1) + S * ((rank + 31) // 32 * 32) * 2
-    dx_bytes = S * K * 2 if p > 0 else 0          # the LoRA term of dX, written once
+    # HIP kernels' algorithmic bytes: the down-projection reads x and writes t
+    # (no dropout output is kept); the dX term is written once; grad_A reads x
+    # again (and d_a) to draw the mask
+    rp = (rank + 31) // 32 * 32
+    down_bytes = S * K * 2 + S * rp * 2
+    dx_bytes = S * K * 2 if p > 0 else 0
+    da_bytes = S * K * 2 + S * rp * 2 + rank * K * 2 if p > 0 else 0
     return {"S": S, "in": K, "out": N, "rank": rank, "dropout": p, "dtype": "bf16",
             "fwd_ms": round(t_f, 4), "bwd_ms": round(t_b, 4), "base_gemm_ms": round(t_gemm, 4),
             "fwd_tflops": round(fl_fwd / (t_f * 1e-3) / 1e12, 1), "bwd_tflops": round(fl_bwd / (t_b * 1e-3) / 1e12, 1),
             "base_gemm_tflops": round(2.0 * S * K * N / (t_gemm * 1e-3) / 1e12, 1),
             "fwd_over_base_gemm": round(t_f / t_gemm, 3),
             "torch_eager_gpu_fwd_bwd_ms": round(t_ref, 4),
-            "kernel_bytes": {"lora_down_kernel": down_bytes, "lora_dx_kernel": dx_bytes},
+            "kernel_bytes": {"lora_down_kernel": down_bytes, "lora_dx_kernel": dx_bytes, "lora_da_kernel": da_bytes},
             "cpu_rows_per_s": round(cpu_rows / cpu_s, 1), "gpu_rows_per_s": round(S / ((t_f + t_b) * 1e-3), 1),
             "cpu_sample": f"the reference's ops as torch eager bf16 on the CPU, fwd + bwd, {cpu_rows} rows, "
                           f"best of 2 after a warm-up, {torch.get_num_threads()} threads"}
