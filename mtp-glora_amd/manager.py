@@ -10,6 +10,13 @@ The BlockMask is built on the GPU from the unclamped gate (pad = -1), and only
 then is the gate clamped and unsqueezed for the LoRA gating (collator.py:208-215).
 The carry-over keeps the chunk's regular-token K/V in the preallocated cache
 in place instead of re-concatenating the prefix.
+
+The reference's ``regular_token_mask.nonzero()`` waits for everything queued
+before it, i.e. the whole forward and backward of the chunk. Here the
+regular-token index is built when the chunk is prepared, before any of the
+chunk's attention work is queued, and its count is copied to pinned host
+memory behind an event; the carry-over waits on that event only, so the host
+goes on queueing the next chunk's kernels while the backward still runs.
 """
 from __future__ import annotations
 
@@ -30,6 +37,8 @@ class StreamingKVCacheManager:
         self.capacity = int(capacity)
         self.sanity_check = sanity_check
         self.cache: StreamingKVCache | None = None
+        self._count_host: torch.Tensor | None = None
+        self._pending = None   # (mask tensor, its version, idx, event)
 
     def reset_cache(self) -> None:
         """Reset KV cache for a new sequence (buffers stay allocated)."""
@@ -58,7 +67,30 @@ class StreamingKVCacheManager:
         bm = build_mtp_block_mask(gate[:1], self.past_seen_tokens)
         chunk_data["attention_mask"] = bm.to(chunk_data["input_ids"].device)
         chunk_data["gate_mask"] = torch.clamp(chunk_data["gate_mask"], min=0)[:, :, None]
+        self._pending = None
+        reg = chunk_data.get("regular_token_mask")
+        if isinstance(reg, torch.Tensor) and reg.is_cuda:
+            idx, cnt = ops.regular_index(reg[0])
+            if self._count_host is None:
+                self._count_host = torch.empty(1, dtype=torch.int32, pin_memory=True)
+            self._count_host.copy_(cnt, non_blocking=True)
+            event = torch.cuda.Event()
+            event.record()
+            self._pending = (reg, reg._version, idx, event)
         return chunk_data
+
+    def _regular_rows(self, reg: torch.Tensor):
+        """(idx, R) of the chunk's regular tokens: from the index
+        built by ``prepare_data_with_kv_cache`` when it was built for this same,
+        unmodified mask (waiting on its event only), else built now with one
+        stream sync, as the reference's nonzero()."""
+        pend, self._pending = self._pending, None
+        if pend is not None and pend[0] is reg and pend[1] == reg._version:
+            _, _, idx, event = pend
+            event.synchronize()
+            return idx, int(self._count_host[0])
+        idx, cnt = ops.regular_index(reg[0])
+        return idx, int(cnt.item())
 
     def extract_regular_kv_cache_for_next_chunk(self, chunk_data: dict, past_key_values=None):
         """Keep only the chunk's regular-token K/V (detached) behind the cached
@@ -70,9 +102,7 @@ class StreamingKVCacheManager:
                           f"but got batch size: {bsz}")
         if past_key_values is None:
             return None
-        reg = chunk_data["regular_token_mask"][0]
-        idx, cnt = ops.regular_index(reg)
-        R = int(cnt.item())   # one host sync, as the reference's nonzero()
+        idx, R = self._regular_rows(chunk_data["regular_token_mask"])
 
         if self.sanity_check and "position_ids" in chunk_data:
             pos = chunk_data["position_ids"][0]

@@ -108,6 +108,35 @@ def test_stream_of_chunks_matches_reference(mga, dev):
         assert torch.equal(a, c_) and torch.equal(b, d)
 
 
+def test_extract_after_mask_changed_in_place(mga, dev):
+    """prepare builds the regular-token index early; a regular_token_mask
+    changed in place between prepare and extract (or replaced by another
+    tensor) must be read again, not served from the early index."""
+    H, D = 2, 64
+    seq = chunk_layout(180, 16, 4, 0, seed=9)
+    S = len(seq.gate)
+    for replace in (False, True):
+        mgr = mga.StreamingKVCacheManager(capacity=1024)
+        cache = mgr.new_cache(1)
+        reg = torch.tensor(seq.regular, device=dev)[None]
+        chunk = {"input_ids": torch.zeros(1, S, dtype=torch.long, device=dev),
+                 "gate_mask": torch.tensor(seq.gate, device=dev)[None], "regular_token_mask": reg}
+        chunk = mgr.prepare_data_with_kv_cache(chunk)
+        k = torch.randn(1, S, H, D, device=dev).bfloat16().transpose(1, 2)
+        cache.update(k, k + 1, 0)
+        changed = reg.clone()
+        changed[0, : S // 3] = 0
+        if replace:
+            chunk["regular_token_mask"] = changed
+        else:
+            reg.copy_(changed)
+        cache = mgr.extract_regular_kv_cache_for_next_chunk(chunk, cache)
+        keep = changed[0].nonzero().flatten()
+        assert mgr.past_seen_tokens == len(keep) == cache.prefix_len
+        kc, vc = cache[0]
+        assert torch.equal(kc, k[:, :, keep]) and torch.equal(vc, (k + 1)[:, :, keep])
+
+
 def test_take_over_dynamic_cache(mga, dev):
     """First chunk through the model's own DynamicCache (past_key_values=None in
     the trainer), then extract moves it into the streaming cache."""
