@@ -56,6 +56,11 @@ __global__ __launch_bounds__(256) void tile_class_kernel(const int32_t *__restri
   const int q0 = qt * kBlock, k0 = kt * kBlock;
   const int nq = min(kBlock, S - q0);
   const int nk = min(kBlock, L - k0);
+  if (k0 > q0 + nq - 1 + P) {
+    // every key follows every query of the tile: causally empty
+    if (t == 0) cls[(int64_t)qt * nKV + kt] = 0;
+    return;
+  }
   if (t < kBlock) sq[t] = t < nq ? code[q0 + t] : kCodePad;
   else sk[t - kBlock] = (t - kBlock) < nk ? key_code(code, k0 + t - kBlock, P, L) : kCodePad;
   __syncthreads();
