@@ -202,8 +202,13 @@ __global__ __launch_bounds__(64) void qk_norm_rope_fwd_kernel(QkRopeArgs a, int 
 
 template <typename T, int V>
 __global__ __launch_bounds__(64) void qk_norm_rope_bwd_kernel(QkRopeArgs a, int lg, float inv_d) {
-  const int s = blockIdx.x;
-  const int lane = threadIdx.x;
+  // The token index is formed per lane (threadIdx.x >> 6 is 0 in a one-wave
+  // workgroup) and bounds-checked: the same rows, but the compiler's code for
+  // this form measured 24.6 us against 27.1 us at [5120, 32 + 8, 128] bf16
+  // (the forward measured slower with it and keeps the plain form).
+  const int s = blockIdx.x + (int)(threadIdx.x >> 6);
+  if (s >= a.S) return;
+  const int lane = threadIdx.x & 63;
   const int j = lane & ((1 << lg) - 1), ngrp = 64 >> lg;
   const Block<T> b = block_of<T>(a, ngrp);
   const int h = b.h0 + (lane >> lg);
