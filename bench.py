@@ -426,9 +426,14 @@ def pmc_pass(torch, mga, libc, q, k, v, do, kp, cache, chunk0, P, S, R, Hkv, D, 
                            True, True, True)
     torch.cuda.synchronize()
     calib = Hkv * CALIB_ROWS * D * 2 * 2
+    a_pre, a_cur = tile_areas(bm, S, L, P)
+    credited = {"attn_fwd_kernel": Hq * D * 4 * (a_pre + a_cur),
+                "attn_bwd_dq_kernel": Hq * D * 6 * (a_pre + a_cur),
+                "attn_bwd_dkdv_kernel": Hq * D * 4 * a_cur}
     print(json.dumps({"pmc_pass": True, "calibration": {"kernel": "kv_copy_rows_kernel",
                                                         "read_bytes": calib, "write_bytes": calib,
-                                                        "grid_rows": CALIB_ROWS}}), flush=True)
+                                                        "grid_rows": CALIB_ROWS},
+                      "credited_flop": credited}), flush=True)
     return 0
 
 

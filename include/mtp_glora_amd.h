@@ -21,6 +21,11 @@
  *     B = H = 1 and 128 x 128 tiles: kv_num[nQ], kv_idx[nQ * nKV] (partial
  *     tiles), full_kv_num / full_kv_idx (full tiles) and the q-major
  *     transposes q_num[nKV], q_idx[nKV * nQ], full_q_num / full_q_idx.
+ *     The attention kernels read them on the device, so they cannot be
+ *     checked before the launch: counts are clamped to [0, n] and indices to
+ *     [0, n - 1] (n = tiles per row). Lists that are not what
+ *     mga_mtp_block_mask writes give wrong results, never an access outside
+ *     the operands.
  */
 #ifndef MTP_GLORA_AMD_H
 #define MTP_GLORA_AMD_H
@@ -53,7 +58,10 @@ const char *mga_last_error(void);
 /*
  * Row copy into the preallocated cache:
  *   dst[h, dst_offset + r, :] = src[h, idx ? idx[r] : r, :]   for r < n_rows, h < n_heads
- * for K and V together.
+ * for K and V together. src_rows: rows of the source per head. Without idx,
+ * n_rows > src_rows is rejected (MGA_ERR_INVALID) before any launch; idx
+ * lives in device memory, so its entries are checked on the device: a row
+ * whose idx[r] falls outside [0, src_rows) is left unwritten.
  * Replaces, with idx == NULL, the torch.cat of DynamicLayer.update
  * ([tf]cache_utils.py:144-146; called at mtp_glora/models/modeling_qwen3.py:284
  * and modeling_llama.py:317), and, with idx = the chunk's regular-token
@@ -62,7 +70,7 @@ const char *mga_last_error(void);
  * Errors: MGA_ERR_CAPACITY when dst_offset + n_rows > dst_capacity.
  */
 int mga_kv_append(const void *src_k, const void *src_v, int64_t src_stride_h, int64_t src_stride_s,
-                  const int32_t *idx, int32_t n_rows,
+                  int64_t src_rows, const int32_t *idx, int32_t n_rows,
                   void *dst_k, void *dst_v, int64_t dst_stride_h, int64_t dst_stride_s,
                   int64_t dst_offset, int64_t dst_capacity,
                   int32_t n_heads, int32_t head_dim, int32_t dtype, void *stream);

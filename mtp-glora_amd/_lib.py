@@ -6,11 +6,14 @@ if it is missing every operation raises, naming the build command.
 from __future__ import annotations
 
 import ctypes
+import os
 import threading
 from pathlib import Path
 
 _HERE = Path(__file__).resolve().parent
-LIB_PATH = _HERE / "lib" / "libmtp_glora_amd.so"
+# MGA_LIBRARY names another build of the same C ABI (e.g. a variant timed
+# against the in-tree one); the default is the in-tree build
+LIB_PATH = Path(os.environ.get("MGA_LIBRARY") or (_HERE / "lib" / "libmtp_glora_amd.so"))
 
 MGA_OK = 0
 MGA_ERR_INVALID = 1
@@ -31,7 +34,7 @@ _U64 = ctypes.c_uint64
 SIGNATURES = {
     "mga_version": [],
     "mga_last_error": [],
-    "mga_kv_append": [_P, _P, _I64, _I64, _P, _I32, _P, _P, _I64, _I64, _I64, _I64, _I32, _I32, _I32, _P],
+    "mga_kv_append": [_P, _P, _I64, _I64, _I64, _P, _I32, _P, _P, _I64, _I64, _I64, _I64, _I32, _I32, _I32, _P],
     "mga_regular_index": [_P, _I64, _I32, _P, _P, _P],
     "mga_mtp_block_mask": [_P, _I64, _I32, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P],
     "mga_attn_fwd": [_P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64,

@@ -36,14 +36,20 @@ def lib_path() -> Path:
     return LIB_DIR / LIB_NAME
 
 
-def build_library(verbose: bool = False, jobs: int = 4) -> Path:
-    """Compile every csrc/*.hip to an object and link the shared library."""
+def build_library(verbose: bool = False, jobs: int = 4, src_dir=None, out_path=None) -> Path:
+    """Compile every csrc/*.hip to an object and link the shared library.
+
+    src_dir / out_path build another source tree (with the same file set) into
+    another library file, e.g. a variant to time against the in-tree build;
+    the default is csrc/ -> lib/libmtp_glora_amd.so."""
     cc = hipcc()
-    objdir = LIB_DIR / "obj"
+    src = Path(src_dir) if src_dir is not None else CSRC
+    out = Path(out_path) if out_path is not None else lib_path()
+    objdir = out.parent / ("obj" if out_path is None else out.stem + "_obj")
     objdir.mkdir(parents=True, exist_ok=True)
-    sources = sorted(CSRC.glob("*.hip"))
+    sources = sorted(src.glob("*.hip"))
     if not sources:
-        raise RuntimeError(f"no HIP sources under {CSRC}")
+        raise RuntimeError(f"no HIP sources under {src}")
 
     def compile_one(src: Path) -> Path:
         obj = objdir / (src.stem + ".o")
@@ -57,7 +63,6 @@ def build_library(verbose: bool = False, jobs: int = 4) -> Path:
 
     with ThreadPoolExecutor(max_workers=jobs) as ex:
         objs = list(ex.map(compile_one, sources))
-    out = lib_path()
     tmp = out.with_suffix(".so.tmp")
     cmd = [cc, "-shared", f"--offload-arch={ARCH}", "-fPIC", *map(str, objs), "-o", str(tmp),
            "-L/opt/rocm/lib", "-lhipblaslt"]

@@ -82,9 +82,9 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(AttnArgs a, int k
 
   const T *qp = reinterpret_cast<const T *>(a.q) + h * a.q_sh;
   const T *dop = reinterpret_cast<const T *>(a.dout) + h * a.do_sh;
-  const int npart = a.q_num[kt];
-  const int ntot = npart + a.fq_num[kt];
-  TileList tiles{a.q_idx + (int64_t)kt * a.nQ, a.fq_idx + (int64_t)kt * a.nQ, npart, ntot};
+  TileList tiles = tile_list(a.q_num, a.q_idx, a.fq_num, a.fq_idx, kt, a.nQ);
+  const int npart = tiles.npart;
+  const int ntot = tiles.ntot;
   const int nstep = 2 * ntot;
   auto step_base = [&](int j) { return tiles.at(j >> 1) * kBlock + (j & 1) * kQStep; };
 

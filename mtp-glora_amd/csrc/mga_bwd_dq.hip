@@ -105,9 +105,9 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnArgs a) {
   const int qv = query_v(qcode);
   const int qlim = (qcode == kCodePad || lse == kNegInfD) ? -1 : row + a.P;
 
-  const int npart = a.kv_num[qt];
-  const int ntot = npart + a.fkv_num[qt];
-  TileList tiles{a.kv_idx + (int64_t)qt * a.nKV, a.fkv_idx + (int64_t)qt * a.nKV, npart, ntot};
+  TileList tiles = tile_list(a.kv_num, a.kv_idx, a.fkv_num, a.fkv_idx, qt, a.nKV);
+  const int npart = tiles.npart;
+  const int ntot = tiles.ntot;
   constexpr int kSub = kBlock / kStep;      // steps per 128-key tile
   const int nstep = kSub * ntot;
   auto step_base = [&](int j) { return tiles.at(j / kSub) * kBlock + (j % kSub) * kStep; };

@@ -20,7 +20,7 @@ constexpr int kCopyThreads = 512;
 __global__ __launch_bounds__(kCopyThreads) void kv_copy_rows_kernel(
     const char *__restrict__ src_k, const char *__restrict__ src_v,
     int64_t src_sh, int64_t src_ss,                 // bytes
-    const int32_t *__restrict__ idx, uint32_t n_rows,
+    const int32_t *__restrict__ idx, int64_t src_rows, uint32_t n_rows,
     char *__restrict__ dst_k, char *__restrict__ dst_v,
     int64_t dst_sh, int64_t dst_ss, int64_t dst_off, // bytes, rows
     uint32_t n_heads, uint32_t vpr_shift) {
@@ -33,20 +33,24 @@ __global__ __launch_bounds__(kCopyThreads) void kv_copy_rows_kernel(
   const uint32_t vmask = (1u << vpr_shift) - 1;
   const uint32_t base = blockIdx.x * (kCopyThreads * kVecPerThread) + threadIdx.x;
   i32x4 buf[kVecPerThread];
+  bool ok[kVecPerThread];
 #pragma unroll
   for (int i = 0; i < kVecPerThread; ++i) {
     const uint32_t w = base + i * kCopyThreads;
-    if (w < per_head) {
+    ok[i] = w < per_head;
+    if (ok[i]) {
       const uint32_t r = w >> vpr_shift;
       const uint32_t vec = w & vmask;
-      const int64_t srow = idx ? idx[r] : (int64_t)r;
-      buf[i] = *reinterpret_cast<const i32x4 *>(src + srow * src_ss + vec * 16);
+      const int64_t srow = idx ? (int64_t)idx[r] : (int64_t)r;
+      // a gather index outside the source leaves its row unwritten
+      ok[i] = srow >= 0 && srow < src_rows;
+      if (ok[i]) buf[i] = *reinterpret_cast<const i32x4 *>(src + srow * src_ss + vec * 16);
     }
   }
 #pragma unroll
   for (int i = 0; i < kVecPerThread; ++i) {
     const uint32_t w = base + i * kCopyThreads;
-    if (w < per_head) {
+    if (ok[i]) {
       const uint32_t r = w >> vpr_shift;
       const uint32_t vec = w & vmask;
       __builtin_nontemporal_store(buf[i], reinterpret_cast<i32x4 *>(dst + (int64_t)r * dst_ss + vec * 16));
@@ -55,7 +59,7 @@ __global__ __launch_bounds__(kCopyThreads) void kv_copy_rows_kernel(
 }
 
 void launch_kv_copy_rows(const void *src_k, const void *src_v, int64_t src_sh_b, int64_t src_ss_b,
-                         const int32_t *idx, int32_t n_rows, void *dst_k, void *dst_v,
+                         int64_t src_rows, const int32_t *idx, int32_t n_rows, void *dst_k, void *dst_v,
                          int64_t dst_sh_b, int64_t dst_ss_b, int64_t dst_off, int32_t n_heads,
                          int32_t row_bytes, hipStream_t stream) {
   uint32_t shift = 0;
@@ -65,7 +69,7 @@ void launch_kv_copy_rows(const void *src_k, const void *src_v, int64_t src_sh_b,
   const uint64_t per_block = (uint64_t)kCopyThreads * kVecPerThread;
   const uint32_t gx = (uint32_t)((per_head + per_block - 1) / per_block);
   hipLaunchKernelGGL(kv_copy_rows_kernel, dim3(gx, 2 * n_heads), dim3(kCopyThreads), 0, stream,
-                     (const char *)src_k, (const char *)src_v, src_sh_b, src_ss_b, idx,
+                     (const char *)src_k, (const char *)src_v, src_sh_b, src_ss_b, idx, src_rows,
                      (uint32_t)n_rows, (char *)dst_k, (char *)dst_v, dst_sh_b, dst_ss_b, dst_off,
                      (uint32_t)n_heads, shift);
 }

@@ -68,7 +68,7 @@ int mga_version(void) { return 100; }
 const char *mga_last_error(void) { return g_err; }
 
 int mga_kv_append(const void *src_k, const void *src_v, int64_t src_stride_h, int64_t src_stride_s,
-                  const int32_t *idx, int32_t n_rows, void *dst_k, void *dst_v,
+                  int64_t src_rows, const int32_t *idx, int32_t n_rows, void *dst_k, void *dst_v,
                   int64_t dst_stride_h, int64_t dst_stride_s, int64_t dst_offset,
                   int64_t dst_capacity, int32_t n_heads, int32_t head_dim, int32_t dtype,
                   void *stream) {
@@ -81,6 +81,9 @@ int mga_kv_append(const void *src_k, const void *src_v, int64_t src_stride_h, in
   if (row_bytes < 16 || (row_bytes & (row_bytes - 1)))
     return fail(MGA_ERR_INVALID, "mga_kv_append: head_dim*elem (%d bytes) must be a power of two >= 16",
                 row_bytes);
+  if (src_rows < 0 || (!idx && n_rows > src_rows))
+    return fail(MGA_ERR_INVALID, "mga_kv_append: %d rows requested from a %lld-row source", n_rows,
+                (long long)src_rows);
   if (dst_offset < 0 || dst_offset + n_rows > dst_capacity)
     return fail(MGA_ERR_CAPACITY, "mga_kv_append: rows [%lld, %lld) exceed the cache capacity %lld",
                 (long long)dst_offset, (long long)(dst_offset + n_rows), (long long)dst_capacity);
@@ -92,7 +95,7 @@ int mga_kv_append(const void *src_k, const void *src_v, int64_t src_stride_h, in
   if ((int64_t)n_rows * (row_bytes / 16) > 0x7fffffffLL)
     return fail(MGA_ERR_INVALID, "mga_kv_append: too many rows per head (%d)", n_rows);
   if (n_rows == 0) { g_err[0] = 0; return MGA_OK; }
-  mga::launch_kv_copy_rows(src_k, src_v, src_stride_h * eb, src_stride_s * eb, idx, n_rows, dst_k,
+  mga::launch_kv_copy_rows(src_k, src_v, src_stride_h * eb, src_stride_s * eb, src_rows, idx, n_rows, dst_k,
                            dst_v, dst_stride_h * eb, dst_stride_s * eb, dst_offset, n_heads,
                            row_bytes, (hipStream_t)stream);
   return check_launch("mga_kv_append");

@@ -278,9 +278,13 @@ namespace mga {
 // The block-mask tile list of one query tile (partial tiles, then full ones),
 // cached 64 entries at a time in a register (lane l holds entry base + l) and
 // read back with readlane, so a step's tile index costs no memory wait.
+// Counts and indices come from the caller's BlockMask tensors: both are
+// clamped into range (counts to [0, n], indices to [0, n - 1]), so malformed
+// metadata gives wrong results but never an access outside the operands.
 struct TileList {
   const int32_t *pidx, *fidx;
   int npart, ntot;
+  int lim;          // number of tiles along the listed axis (n)
   int base = -64;
   int val = 0;
 
@@ -289,6 +293,7 @@ struct TileList {
     if (cb != base) {
       const int e = cb + (threadIdx.x & 63);
       val = e < npart ? pidx[e] : (e < ntot ? fidx[e - npart] : 0);
+      val = min(max(val, 0), lim - 1);
       base = cb;
       // wait for the refill here (once per 64 tiles): left to the use, the
       // wait would sit on every call and drain all loads in flight
@@ -297,6 +302,15 @@ struct TileList {
     return __builtin_amdgcn_readlane(val, it & 63);
   }
 };
+
+// Tile list of row r of a BlockMask: partial tiles pidx[r * n ..], count
+// pnum[r]; full tiles fidx[r * n ..], count fnum[r]; n tiles per row.
+__device__ __forceinline__ TileList tile_list(const int32_t *pnum, const int32_t *pidx, const int32_t *fnum,
+                                              const int32_t *fidx, int r, int n) {
+  const int np = min(max(pnum[r], 0), n);
+  const int nf = min(max(fnum[r], 0), n - np);
+  return TileList{pidx + (int64_t)r * n, fidx + (int64_t)r * n, np, np + nf, n};
+}
 
 }  // namespace mga
 

@@ -115,9 +115,9 @@ __global__ __launch_bounds__(256, 3 - NB) void attn_fwd_kernel(AttnArgs a) {
     qlim[nb] = (qcode == kCodePad) ? -1 : row + a.P;
   }
 
-  const int npart = a.kv_num[qt];
-  const int ntot = npart + a.fkv_num[qt];
-  TileList tiles{a.kv_idx + (int64_t)qt * a.nKV, a.fkv_idx + (int64_t)qt * a.nKV, npart, ntot};
+  TileList tiles = tile_list(a.kv_num, a.kv_idx, a.fkv_num, a.fkv_idx, qt, a.nKV);
+  const int npart = tiles.npart;
+  const int ntot = tiles.ntot;
   const int nstep = kStepsPerTile * ntot;
   auto step_base = [&](int j) { return tiles.at(j / kStepsPerTile) * kBlock + (j % kStepsPerTile) * kStepKeys; };
 

@@ -27,7 +27,7 @@ struct AttnArgs {
 };
 
 void launch_kv_copy_rows(const void *src_k, const void *src_v, int64_t src_sh_b, int64_t src_ss_b,
-                         const int32_t *idx, int32_t n_rows, void *dst_k, void *dst_v,
+                         int64_t src_rows, const int32_t *idx, int32_t n_rows, void *dst_k, void *dst_v,
                          int64_t dst_sh_b, int64_t dst_ss_b, int64_t dst_off, int32_t n_heads,
                          int32_t row_bytes, hipStream_t stream);
 

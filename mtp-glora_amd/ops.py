@@ -86,7 +86,7 @@ def kv_append(src_k: torch.Tensor, src_v: torch.Tensor, dst_k: torch.Tensor, dst
         rows = int(idx.numel()) if n_rows is None else int(n_rows)
     else:
         rows = sk.shape[1] if n_rows is None else int(n_rows)
-    _lib.call("mga_kv_append", sk.data_ptr(), sv.data_ptr(), ssh, sss,
+    _lib.call("mga_kv_append", sk.data_ptr(), sv.data_ptr(), ssh, sss, sk.shape[1],
               idx.data_ptr() if idx is not None else None, rows,
               dst_k.data_ptr(), dst_v.data_ptr(), dst_k.stride(0), dst_k.stride(1),
               int(dst_offset), cap, H, D, dtype_code(dst_k.dtype), _stream(dst_k))

@@ -10,9 +10,17 @@
   Each kernel's figure is its last dispatch in the pass (the hot-path launch;
   set-up work such as the prefix fill runs before it).
 
+* ``mfma``: ``--pmc`` runs of ``bench.py --pmc-pass`` collecting SQ and GRBM
+  counters (any number of runs, each its own CSV) turned into per-kernel
+  figures for the attention kernels: MFMA busy fraction (busy cycles of the
+  MFMA units over all SIMDs' active cycles), the bf16 MFMA work the counters
+  count against the credited work, and instructions per MFMA.
+
     python mtp-glora_amd/rocprof_summary.py stats TRACE_DIR/bench_kernel_stats.csv
     python mtp-glora_amd/rocprof_summary.py traffic --fetch F.csv --write W.csv \\
         --calib-read BYTES --calib-write BYTES --config 2 -o profiles/config2_traffic.json
+    python mtp-glora_amd/rocprof_summary.py mfma --pass-json PASS.json A.csv B.csv \\
+        -o profiles/config2_mfma.json
 """
 from __future__ import annotations
 
@@ -75,6 +83,61 @@ def traffic(fetch_csv: str, write_csv: str, calib_read: int, calib_write: int, c
     return result
 
 
+SIMDS = 1024          # MI355X: 256 CUs x 4 SIMDs
+XCDS = 8              # GRBM_GUI_ACTIVE is summed over the 8 XCDs in the CSV
+MOP_FLOP = 512        # one SQ_INSTS_VALU_MFMA_MOPS_* unit (FLOP)
+ATTN_KERNELS = ("attn_fwd_kernel", "attn_bwd_dq_kernel", "attn_bwd_dkdv_kernel")
+
+
+def counters_by_kernel(paths) -> dict:
+    """{kernel: {counter: value}} from the last dispatch of each kernel in
+    every counter CSV (one rocprofv3 --pmc run each)."""
+    out: dict = {}
+    for path in paths:
+        last: dict = {}
+        for r in csv.DictReader(open(path)):
+            k = kernel_base(r["Kernel_Name"])
+            d = int(r["Dispatch_Id"])
+            cur = last.setdefault(k, {})
+            cur.setdefault(d, {})[r["Counter_Name"]] = float(r["Counter_Value"])
+        for k, per in last.items():
+            out.setdefault(k, {}).update(per[max(per)])
+    return out
+
+
+def mfma_summary(paths, credited: dict) -> dict:
+    c = counters_by_kernel(paths)
+    res = {"simds": SIMDS, "xcds": XCDS, "mop_flop": MOP_FLOP, "kernels": {}}
+    for k in ATTN_KERNELS:
+        if k not in c:
+            continue
+        v = c[k]
+        e = {"counters": v}
+        gui = v.get("GRBM_GUI_ACTIVE")
+        if gui and "SQ_VALU_MFMA_BUSY_CYCLES" in v:
+            e["mfma_busy_frac"] = v["SQ_VALU_MFMA_BUSY_CYCLES"] / (gui / XCDS * SIMDS)
+        if "SQ_VALU_MFMA_BUSY_CYCLES" in v and "SQ_BUSY_CU_CYCLES" in v and v["SQ_BUSY_CU_CYCLES"]:
+            e["mfma_busy_per_busy_cu_simd"] = v["SQ_VALU_MFMA_BUSY_CYCLES"] / (4 * v["SQ_BUSY_CU_CYCLES"])
+        if "SQ_INSTS_VALU_MFMA_MOPS_BF16" in v:
+            fl = v["SQ_INSTS_VALU_MFMA_MOPS_BF16"] * MOP_FLOP
+            e["mfma_flop"] = fl
+            if credited.get(k):
+                e["credited_flop"] = credited[k]
+                e["mfma_flop_over_credited"] = fl / credited[k]
+        n_mfma = v.get("SQ_INSTS_MFMA") or v.get("SQ_INSTS_VALU_MFMA_BF16")
+        if n_mfma:
+            for name in ("SQ_INSTS_VALU", "SQ_INSTS_SALU", "SQ_INSTS_LDS", "SQ_INSTS_VALU_TRANS_F32"):
+                if name in v:
+                    e[name[9:].lower() + "_per_mfma"] = v[name] / n_mfma
+        if v.get("SQ_WAVE_CYCLES"):
+            for name in ("SQ_WAIT_INST_ANY", "SQ_WAIT_INST_LDS", "SQ_ACTIVE_INST_VALU", "SQ_ACTIVE_INST_LDS",
+                         "SQ_WAIT_ANY"):
+                if name in v:
+                    e[name[3:].lower() + "_frac_of_wave_cycles"] = v[name] / v["SQ_WAVE_CYCLES"]
+        res["kernels"][k] = e
+    return res
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     sub = ap.add_subparsers(dest="cmd", required=True)
@@ -87,11 +150,24 @@ def main(argv=None) -> int:
     t.add_argument("--calib-write", type=int, required=True)
     t.add_argument("--config", type=int, default=2)
     t.add_argument("-o", "--out")
+    m = sub.add_parser("mfma")
+    m.add_argument("csvs", nargs="+")
+    m.add_argument("--pass-json", help="the JSON line bench.py --pmc-pass printed (credited FLOPs)")
+    m.add_argument("-o", "--out")
     args = ap.parse_args(argv)
     if args.cmd == "stats":
         print(stats_markdown(args.csv))
         return 0
-    res = traffic(args.fetch, args.write, args.calib_read, args.calib_write, args.config)
+    if args.cmd == "mfma":
+        credited = {}
+        if args.pass_json:
+            for line in open(args.pass_json):
+                line = line.strip()
+                if line.startswith("{") and "pmc_pass" in line:
+                    credited = json.loads(line).get("credited_flop", {})
+        res = mfma_summary(args.csvs, credited)
+    else:
+        res = traffic(args.fetch, args.write, args.calib_read, args.calib_write, args.config)
     text = json.dumps(res, indent=1)
     if args.out:
         with open(args.out, "w") as f:

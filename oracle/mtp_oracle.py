@@ -11,6 +11,9 @@ installed torch / transformers trees):
 * ``synth_sequence`` / ``synth_chunk``   - token layout of
   ``mtp_glora/data_utils/dataset.py:25-56`` (anchor followed by its D mask
   tokens; positions; gate / regular masks) for seeded synthetic inputs.
+* ``insert_mask_tokens``                 - the dataset's own layout of one
+  example (dataset.py:25-56): every response token an anchor, labels by the
+  position + 1 gather, so the last blocks are partly labelled.
 * ``split_points`` / ``pick_last_bucket`` / ``chunk_sequence`` - chunking and
   padding of ``mtp_glora/data_utils/collator.py:73-175``.
 * ``mtp_mask_dense``                     - the MTP ``mask_mod`` predicate of
@@ -37,7 +40,6 @@ Parity pins for every function live in ``tests/test_oracle_*.py``.
 """
 from __future__ import annotations
 
-import math
 from dataclasses import dataclass
 
 import numpy as np
@@ -109,6 +111,36 @@ def synth_sequence(n_regular: int, anchors: np.ndarray, draft_length: int,
                 block[t] = b
                 t += 1
             b += 1
+    return Sequence(gate, regular, position, block, is_anchor)
+
+
+def insert_mask_tokens(input_len: int, output_len: int, draft_length: int) -> Sequence:
+    """The token layout the reference's dataset builds for one example
+    (``insert_mask_tokens``, dataset.py:25-56): ``input_len`` prompt tokens,
+    then every one of the ``output_len`` response tokens followed by its
+    ``draft_length`` mask tokens (every response token is an anchor).
+
+    Positions (dataset.py:30-36): the prompt gets 0 .. input_len - 1; response
+    token j and its masks get input_len + j + (0 .. D). Labels (dataset.py:38-41)
+    are the label row ``[-100] * input_len ++ response ++ [-100] * (D + 1)``
+    gathered at position + 1. gate = 1 on a mask token whose label is not
+    -100, else 0 (dataset.py:53); regular = 1 on non-mask tokens (:54).
+    """
+    D = int(draft_length)
+    n_in, n_out = int(input_len), int(output_len)
+    blk = (np.arange(n_out)[:, None] + np.arange(D + 1)[None, :]).reshape(-1)
+    position = np.concatenate([np.arange(n_in), blk + n_in]).astype(np.int64)
+    response = np.arange(1, n_out + 1, dtype=np.int64)          # any ids other than -100
+    label_row = np.concatenate([np.full(n_in, -100, np.int64), response,
+                                np.full(D + 1, -100, np.int64)])
+    labels = label_row[position + 1]
+    is_mask = np.concatenate([np.zeros(n_in, bool),
+                              np.tile(np.arange(D + 1) > 0, n_out)])
+    gate = np.where(is_mask & (labels != -100), 1, 0).astype(np.int64)
+    regular = (~is_mask).astype(np.int64)
+    block = np.concatenate([np.full(n_in, -1, np.int64),
+                            np.repeat(np.arange(n_out, dtype=np.int64), D + 1)])
+    is_anchor = np.concatenate([np.zeros(n_in, bool), np.tile(np.arange(D + 1) == 0, n_out)])
     return Sequence(gate, regular, position, block, is_anchor)
 
 
@@ -487,17 +519,3 @@ def credited_flops(bm: dict, S: int, L: int, P: int, Hq: int, D: int):
     fwd = Hq * D * 4 * (a_pre + a_cur)
     bwd = Hq * D * (6 * a_pre + 10 * a_cur)
     return fwd, bwd
-
-
-def to_bf16(x: np.ndarray) -> np.ndarray:
-    """Round float32 values to bfloat16 (round to nearest even), returned as float32."""
-    x = np.asarray(x, np.float32)
-    u = x.view(np.uint32).astype(np.uint64)
-    lsb = (u >> 16) & 1
-    u = (u + 0x7FFF + lsb) & 0xFFFF0000
-    out = u.astype(np.uint32).view(np.float32)
-    return np.where(np.isnan(x), x, out)
-
-
-def lse_to_log2(lse: np.ndarray) -> np.ndarray:
-    return lse / math.log(2.0)

@@ -40,12 +40,26 @@ def f64(t):
     return t.detach().double().cpu().numpy()
 
 
-def check(name, got, ref, max_abs=MAX_ABS, mean_abs=MEAN_ABS):
-    err = np.abs(np.asarray(got, np.float64) - np.asarray(ref, np.float64))
+def check(name, got, ref, max_abs=MAX_ABS, mean_abs=MEAN_ABS, scale_above_one=False):
+    """max |got - ref| <= max_abs and mean |got - ref| <= mean_abs.
+
+    scale_above_one: the max bound applies to |got - ref| / max(1, |ref|),
+    i.e. absolute where |ref| <= 1 and relative above. For a bf16 output of
+    magnitude 4..8 one rounding alone is up to 2^-6 = 0.0156, and the bf16
+    probabilities the dV / dK products multiply add about as much again, so
+    the absolute 2e-2 is then below what any bf16 implementation (the
+    reference's flex path included) can meet; the mean bound stays absolute."""
+    g = np.asarray(got, np.float64)
+    r = np.asarray(ref, np.float64)
+    err = np.abs(g - r)
     mx, mn = float(err.max()) if err.size else 0.0, float(err.mean()) if err.size else 0.0
-    print(f"  {name}: max-abs {mx:.3e} mean-abs {mn:.3e}", flush=True)
+    lim = err / np.maximum(1.0, np.abs(r)) if scale_above_one else err
+    mxs = float(lim.max()) if lim.size else 0.0
+    big = float(np.abs(r).max()) if r.size else 0.0
+    print(f"  {name}: max-abs {mx:.3e} mean-abs {mn:.3e}"
+          + (f" max-abs/max(1,|ref|) {mxs:.3e} (max |ref| {big:.2f})" if scale_above_one else ""), flush=True)
     assert np.isfinite(got).all(), f"{name} has non-finite values"
-    assert mx <= max_abs and mn <= mean_abs, f"{name}: max-abs {mx:.3e} mean-abs {mn:.3e}"
+    assert mxs <= max_abs and mn <= mean_abs, f"{name}: max-abs {mx:.3e} ({mxs:.3e}) mean-abs {mn:.3e}"
 
 
 def torch_dense_reference(q, kfull, vfull, allowed, scale, do=None, grad_start=0):

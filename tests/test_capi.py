@@ -42,10 +42,10 @@ def test_version_and_empty_error(mga):
 
 
 def _append(lib, **kw):
-    a = dict(src_k=16, src_v=16, sh=1024, ss=128, idx=None, n=4, dk=16, dv=16, dsh=1024,
+    a = dict(src_k=16, src_v=16, sh=1024, ss=128, src_rows=8, idx=None, n=4, dk=16, dv=16, dsh=1024,
              dss=128, off=0, cap=8, heads=2, hd=128, dtype=0, stream=None)
     a.update(kw)
-    return lib.mga_kv_append(a["src_k"], a["src_v"], a["sh"], a["ss"], a["idx"], a["n"], a["dk"],
+    return lib.mga_kv_append(a["src_k"], a["src_v"], a["sh"], a["ss"], a["src_rows"], a["idx"], a["n"], a["dk"],
                              a["dv"], a["dsh"], a["dss"], a["off"], a["cap"], a["heads"], a["hd"],
                              a["dtype"], a["stream"])
 
@@ -57,7 +57,8 @@ def test_append_capacity_error(mga):
 
 
 @pytest.mark.parametrize("kw", [dict(dtype=7), dict(hd=48), dict(src_k=None), dict(src_k=8),
-                                dict(ss=3), dict(heads=0), dict(n=-1)])
+                                dict(ss=3), dict(heads=0), dict(n=-1),
+                                dict(src_rows=3), dict(src_rows=-1)])
 def test_append_invalid_arguments(mga, kw):
     lib = mga.load_library()
     assert _append(lib, **kw) == mga._lib.MGA_ERR_INVALID
@@ -81,4 +82,4 @@ def test_attention_invalid_arguments(mga):
 
 def test_python_errors_are_raised(mga):
     with pytest.raises(mga._lib.CapacityError):
-        mga._lib.call("mga_kv_append", 16, 16, 1024, 128, None, 4, 16, 16, 1024, 128, 6, 8, 2, 128, 0, None)
+        mga._lib.call("mga_kv_append", 16, 16, 1024, 128, 8, None, 4, 16, 16, 1024, 128, 6, 8, 2, 128, 0, None)

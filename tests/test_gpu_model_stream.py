@@ -4,6 +4,12 @@ vocab 1024, fp32) with Gated LoRA (rank 8) on q/k/v/o, trained over an MTP
 sequence in chunks exactly as the reference's chunk loop drives it
 (mtp_glora/trainer/trainer.py:95-136): reset -> per chunk prepare (BlockMask)
 -> forward with the cache -> loss.backward -> extract the regular-token K/V.
+The same stream also runs through transformers' LlamaForCausalLM, the Llama
+call site (modeling_llama.py:292-332): there the first chunk gets
+past_key_values=None, so the model makes its own DynamicCache
+(modeling_llama.py:451-452) and the manager takes it over, and the attention
+is found under the reference's own key "flex_attention"
+(trainer/utils.py:68) after register(replace_flex=True).
 
 The HIP path runs through the drop-in boundary only: the attention function
 registered with transformers, StreamingKVCache as past_key_values and
@@ -30,7 +36,8 @@ from oracle import mtp_oracle as mo
 pytestmark = pytest.mark.gpu
 
 transformers = pytest.importorskip("transformers")
-from transformers import AttentionInterface, Qwen3Config, Qwen3ForCausalLM  # noqa: E402
+from transformers import (AttentionInterface, LlamaConfig, LlamaForCausalLM, Qwen3Config,  # noqa: E402
+                          Qwen3ForCausalLM)
 from transformers.cache_utils import DynamicCache  # noqa: E402
 
 N_REG, N_CHUNKS, N_ANCHOR, DRAFT, RANK, VOCAB = 1024, 4, 16, 4, 8, 1024
@@ -67,13 +74,14 @@ def dense_masked_attention(module, query, key, value, attention_mask, scaling=No
     return (p @ v).transpose(1, 2).contiguous(), None
 
 
-def build_model(attn: str, dtype, device, seed: int = 0):
-    cfg = Qwen3Config(vocab_size=VOCAB, hidden_size=256, intermediate_size=512, num_hidden_layers=2,
-                      num_attention_heads=4, num_key_value_heads=2, head_dim=64,
-                      max_position_embeddings=4096, tie_word_embeddings=False)
+def build_model(attn: str, dtype, device, seed: int = 0, family: str = "qwen3"):
+    dims = dict(vocab_size=VOCAB, hidden_size=256, intermediate_size=512, num_hidden_layers=2,
+                num_attention_heads=4, num_key_value_heads=2, head_dim=64,
+                max_position_embeddings=4096, tie_word_embeddings=False)
+    cfg = Qwen3Config(**dims) if family == "qwen3" else LlamaConfig(**dims)
     cfg._attn_implementation = attn
     torch.manual_seed(seed)
-    model = Qwen3ForCausalLM(cfg)
+    model = Qwen3ForCausalLM(cfg) if family == "qwen3" else LlamaForCausalLM(cfg)
     gen = torch.Generator().manual_seed(seed + 1)
     loras = []
     for layer in model.model.layers:
@@ -109,11 +117,14 @@ def chunk_loss(logits, labels):
     return torch.nn.functional.cross_entropy(logits[0].float(), labels, reduction="sum") / labels.numel()
 
 
-def run_hip(mga, chunks, dev):
-    model, loras = build_model("mtp_hip", torch.float32, dev)
+def run_hip(mga, chunks, dev, family="qwen3", attn="mtp_hip"):
+    model, loras = build_model(attn, torch.float32, dev, family=family)
     mgr = mga.StreamingKVCacheManager(capacity=4096)
     mgr.reset_cache()
-    pkv = mgr.new_cache(num_layers=2)
+    # Qwen3: the manager's cache from the first chunk on; Llama: None, as the
+    # reference trainer passes it (trainer.py:100), so the model builds a
+    # DynamicCache that the first carry-over takes over
+    pkv = mgr.new_cache(num_layers=2) if family == "qwen3" else None
     logits_out = []
     for c, (seq, ids, labels) in enumerate(chunks):
         chunk = {"input_ids": torch.tensor(ids, device=dev)[None],
@@ -135,8 +146,8 @@ def run_hip(mga, chunks, dev):
     return logits_out, grads
 
 
-def run_reference(chunks):
-    model, loras = build_model("mtp_dense_ref", torch.float64, "cpu")
+def run_reference(chunks, family="qwen3"):
+    model, loras = build_model("mtp_dense_ref", torch.float64, "cpu", family=family)
     pkv = None
     P = 0
     logits_out = []
@@ -162,9 +173,9 @@ def run_reference(chunks):
     return logits_out, grads
 
 
-def run_single_pass(chunks):
+def run_single_pass(chunks, family="qwen3"):
     """One forward over the whole sequence with the full MTP mask."""
-    model, loras = build_model("mtp_dense_ref", torch.float64, "cpu")
+    model, loras = build_model("mtp_dense_ref", torch.float64, "cpu", family=family)
     gate_all = np.concatenate([s.gate for s, _, _ in chunks])
     ids = np.concatenate([i for _, i, _ in chunks])
     pos = np.concatenate([s.position for s, _, _ in chunks])
@@ -183,18 +194,28 @@ def _check(name, got, ref, max_abs, mean_abs):
     assert err.max().item() <= max_abs and err.mean().item() <= mean_abs, name
 
 
-def _stream_against_reference(dev, fused_qk_norm_rope: bool, monkeypatch):
+def _stream_against_reference(dev, fused_qk_norm_rope: bool, monkeypatch, family="qwen3"):
     mga = importlib.import_module("mtp-glora_amd")
-    mga.register("mtp_hip")
     AttentionInterface.register("mtp_dense_ref", dense_masked_attention)
     chunks = make_sequence(0)
     with monkeypatch.context() as m:
+        if family == "llama":
+            # the reference's attn_implementation="flex_attention" finds the
+            # HIP attention; the original entry comes back after the test
+            from transformers.modeling_utils import ALL_ATTENTION_FUNCTIONS
+            m.setitem(ALL_ATTENTION_FUNCTIONS._global_mapping, "flex_attention",
+                      ALL_ATTENTION_FUNCTIONS._global_mapping["flex_attention"])
+            mga.register("mtp_hip", replace_flex=True)
+            attn = "flex_attention"
+        else:
+            mga.register("mtp_hip")
+            attn = "mtp_hip"
         if fused_qk_norm_rope:
             from transformers.models.qwen3 import modeling_qwen3
             m.setattr(modeling_qwen3.Qwen3Attention, "forward", mga.qwen3_attention_forward)
-        hip_logits, hip_grads = run_hip(mga, chunks, dev)
-    ref_logits, ref_grads = run_reference(chunks)
-    one_pass = run_single_pass(chunks)
+        hip_logits, hip_grads = run_hip(mga, chunks, dev, family=family, attn=attn)
+    ref_logits, ref_grads = run_reference(chunks, family=family)
+    one_pass = run_single_pass(chunks, family=family)
     for c in range(len(chunks)):
         # chunk equivalence of the reference itself, then the HIP stream against both
         assert torch.allclose(ref_logits[c], one_pass[c], atol=1e-9, rtol=0)
@@ -214,3 +235,10 @@ def test_config1_chunk_stream_with_fused_qk_norm_rope(dev, monkeypatch):
     runs q_norm / k_norm / rope as one HIP kernel (forward and backward): the
     LoRA gradients of q_proj and k_proj flow through its backward."""
     _stream_against_reference(dev, True, monkeypatch)
+
+
+def test_config1_chunk_stream_through_transformers_llama(dev, monkeypatch):
+    """The Llama call site: LlamaAttention.forward's cache update and attention
+    lookup, the model's own DynamicCache on the first chunk, and the HIP
+    attention registered under "flex_attention"."""
+    _stream_against_reference(dev, False, monkeypatch, family="llama")
