@@ -127,10 +127,9 @@ int mga_attn_fwd(const void *q, int64_t q_sh, int64_t q_ss,
  *   dk, dv [Hkv, L - grad_start, D] for keys j >= grad_start only, summed over
  *   the G query heads of each kv head. With grad_start = P the detached
  *   prefix (collator.py:279-280) gets no gradient and costs no dK/dV work.
- * delta: workspace of Hq * S floats (rowsum(o * dout)), written by the dQ pass.
- * dkv_ws: fp32 workspace of 2 * G * (L - grad_start) * Hkv * head_dim floats
- *   (G = Hq / Hkv) holding per-query-head dK/dV partials that are then summed
- *   in a fixed order; required for the dK/dV pass when G > 1, else may be NULL.
+ * delta: workspace of Hq * S floats (rowsum(o * dout)), written by the dQ pass
+ *   and read by the dK/dV pass. dK/dV are summed over the G query heads inside
+ *   the pass, in a fixed order (no other workspace, no atomics).
  * passes: MGA_BWD_DQ | MGA_BWD_DKDV for the full backward. MGA_BWD_DQ alone
  *   serves a caller whose K/V need no gradient; the passes may also be issued
  *   as two calls in stream order (MGA_BWD_DQ first: it writes delta).
@@ -143,7 +142,7 @@ int mga_attn_bwd(const void *q, int64_t q_sh, int64_t q_ss,
                  const void *v, int64_t v_sh, int64_t v_ss,
                  const void *o, int64_t o_sh, int64_t o_ss,
                  const void *dout, int64_t do_sh, int64_t do_ss,
-                 const float *lse, float *delta, float *dkv_ws,
+                 const float *lse, float *delta,
                  void *dq, int64_t dq_sh, int64_t dq_ss,
                  void *dk, int64_t dk_sh, int64_t dk_ss,
                  void *dv, int64_t dv_sh, int64_t dv_ss,

@@ -41,7 +41,7 @@ SIGNATURES = {
                      _P, _P, _P, _P, _P, _P,
                      _I32, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _P],
     "mga_attn_bwd": [_P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64,
-                     _P, _P, _P,
+                     _P, _P,
                      _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64,
                      _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                      _I32, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _I32, _P],

@@ -1,17 +1,26 @@
 // MTP block-masked GQA attention backward, dK/dV pass, for gfx950.
 //
-// Work item = (128-key tile of the keys that receive gradient, query head h).
-// Each of the 4 waves owns 32 keys and keeps their K and V rows in registers
-// (B operands). The workgroup walks the q-major block-mask list of its key
-// tile; per 64-row query step of head h (Q and dO staged by direct
-// global -> LDS loads into double buffers) each wave computes
-//   S  = Q K^T,  dP = dO V^T                  (A operands: Q, dO rows)
-//   P  = exp2(S * scale_log2 - lse_log2)       (0 where masked)
-//   dS = P (dP - delta)
-//   dV^T += dO^T P,  dK^T += Q^T dS            (A operands by transpose read)
-// With one query head per kv head (G = 1) the result is written directly;
-// otherwise each head writes an fp32 partial and dkdv_reduce_kernel sums the
-// G partials of a kv head in a fixed order (deterministic, no atomics).
+// Work item = (64-key tile of the keys that receive gradient, kv head g): one
+// workgroup of 8 waves, 2 per SIMD. The G query heads of g and the q-major
+// block-mask list of the key tile give a list of (query tile, head) pairs;
+// the two 4-wave groups of the workgroup take alternate pairs, 32 query rows
+// per step. Within a group each 32-key half of the tile belongs to a pair of
+// waves that split the four products between them:
+//   wave A holds K in registers:  S = Q K^T (accumulator starting at
+//       -lse / scale, so P = exp2(scale_log2 * S)), 0 where masked,
+//       dV^T += dO^T P                       (A operand dO^T by transpose read)
+//   wave B holds V in registers:  dP = dO V^T (starting at -delta),
+//       dS = P dP with A's P read back from LDS,
+//       dK^T += Q^T dS                       (A operand Q^T by transpose read)
+// so each wave keeps one 32 x HD accumulator and one operand set (about 200
+// registers) and two waves share a SIMD. B runs its dS / dK part one step
+// behind A: A's P crosses LDS under the one barrier per step that also
+// rotates the staging buffers. The Q / dO tiles of step j + 2 are loaded
+// (global -> LDS) while step j computes, their row data one step ahead: four
+// Q buffers (B's dK of step j - 1 reads Q(j - 1)) and four dO buffers. At the end group 1 hands its
+// accumulators to group 0 through LDS and group 0 adds them in a fixed order:
+// dK and dV summed over the G heads without partial sums in global memory or
+// atomics, and bit-for-bit repeatable.
 // Semantics: [torch]_higher_order_ops/flex_attention.py:826-990 (dK/dV summed
 // over the query heads of a kv head, :957-966), restricted to keys >= grad_start.
 #include <type_traits>
@@ -24,11 +33,16 @@ namespace mga {
 namespace {
 
 constexpr float kNegInfK = -__builtin_huge_valf();
-constexpr int kQStep = 64;
+constexpr int kRows = 32;         // query rows per step
+constexpr int kKeys = 64;         // keys per workgroup
+constexpr int kThreads = 512;
+// ordered-compare values of this pass: a pad query (or a row past S) sits
+// above every key, a regular key and a regular query one below
+constexpr int kVRegular = 0x7ffffffe;
+constexpr int kVPadQuery = 0x7fffffff;
 
 typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2;
 
-// two values -> one packed bf16 pair (round to nearest even)
 __device__ __forceinline__ uint32_t cvt2(float x, float y) {
   bf16x2 v;
   v[0] = (bf16_t)x;
@@ -36,297 +50,432 @@ __device__ __forceinline__ uint32_t cvt2(float x, float y) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
+// Per-step bookkeeping of one group, carried from the load to the compute.
+struct StepInfo {
+  int q0;       // first query row (chunk index)
+  int h;        // query head
+  int flags;    // 1: rows exist (step active), 2: partial tile (masking)
+};
+
+// 16 per-row values of a 32-row block in accumulator order: register r holds
+// row 8 (r / 4) + 4 hi + r % 4, four consecutive rows per 16-byte read; ofs is
+// the lane's byte offset of row 4 hi (plus the group's block).
+__device__ __forceinline__ f32x16 rows16(const float *t, uint32_t ofs) {
+  f32x16 v;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const f32x4 x = *reinterpret_cast<const f32x4 *>(lds_at(t, ofs + 32 * i));
+    v[4 * i] = x[0]; v[4 * i + 1] = x[1]; v[4 * i + 2] = x[2]; v[4 * i + 3] = x[3];
+  }
+  return v;
+}
+
+// Global -> LDS staging of a 32 x HD tile by the 4 waves of a group (w4:
+// the wave within the group, gt: the thread within the group); rows past
+// rmax repeat row rmax. bf16: direct loads (completion on vmcnt); fp32:
+// through registers, converted to bf16 at store time.
+template <int HD, typename T>
+struct GroupTile {
+  static constexpr int kGran = kRows * HD / 8 / 256;
+  static constexpr int kInst = kRows / (64 / (HD / 8)) / 4;   // direct loads per wave (bf16)
+  i32x4 reg[sizeof(T) == 2 ? 1 : kGran];
+
+  __device__ __forceinline__ void load(bf16_t *tile, const T *src, int64_t ss, int r0, int rmax, int w4, int gt) {
+    if constexpr (sizeof(T) == 2) {
+      constexpr int kGranRow = HD / 8;
+      constexpr int kRowsPerInst = 64 / kGranRow;
+      constexpr int kInst = kRows / kRowsPerInst / 4;
+      const int lane = gt & 63, p = lane % kGranRow;
+#pragma unroll
+      for (int i = 0; i < kInst; ++i) {
+        const int blk = w4 * kInst + i;
+        const int r = blk * kRowsPerInst + lane / kGranRow;
+        const int c = p ^ swz<HD>(r);
+        const int row = min(r0 + r, rmax);
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const bf16_t *>(src) + (int64_t)row * ss + c * 8,
+                                         (lds_void *)(tile + blk * 512), 16, 0, 0);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < kGran; ++i) {
+        const int gi = gt + 256 * i;
+        const int r = gi / (HD / 8), c = gi % (HD / 8);
+        reg[i] = __builtin_bit_cast(i32x4, load8(src + (int64_t)min(r0 + r, rmax) * ss + c * 8));
+      }
+    }
+  }
+  __device__ __forceinline__ void store(bf16_t *tile, int gt) const {
+    if constexpr (sizeof(T) != 2) {
+#pragma unroll
+      for (int i = 0; i < kGran; ++i) {
+        const int gi = gt + 256 * i;
+        const int r = gi / (HD / 8), c = gi % (HD / 8);
+        *reinterpret_cast<i32x4 *>(tile + tile_off<HD>(r, c)) = reg[i];
+      }
+    }
+  }
+};
+
 }  // namespace
 
 template <int HD, typename T>
-__global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(AttnArgs a, int kt0, int nkt) {
+__global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_kernel(AttnArgs a, int kh0, int nkh) {
   constexpr int KS = HD / 16;
   constexpr int DB = HD / 32;
-  constexpr int TILE = kQStep * HD;
-  __shared__ __attribute__((aligned(16))) bf16_t sQ0[TILE], sQ1[TILE];
-  __shared__ __attribute__((aligned(16))) bf16_t sD0[TILE], sD1[TILE];
-  // per query row of the step: lse * log2(e), delta, causal bound (-1: sees nothing),
-  // ordered-compare value (query_v)
-  __shared__ __attribute__((aligned(16))) float sL0[kQStep], sL1[kQStep];
-  __shared__ __attribute__((aligned(16))) float sE0[kQStep], sE1[kQStep];
-  __shared__ __attribute__((aligned(16))) int sM0[kQStep], sM1[kQStep];
-  __shared__ __attribute__((aligned(16))) int sC0[kQStep], sC1[kQStep];
+  constexpr int TILE = kRows * HD;          // one group's tile (elements)
+  // staging buffers, each holding both groups' tiles ([group][TILE]); named
+  // objects so the compiler sees that the direct loads into one never alias
+  // the reads of another (the step loop is unrolled to make every index a
+  // constant)
+  __shared__ __attribute__((aligned(16))) bf16_t sQ0[2 * TILE], sQ1[2 * TILE], sQ2[2 * TILE], sQ3[2 * TILE];
+  __shared__ __attribute__((aligned(16))) bf16_t sD0[2 * TILE], sD1[2 * TILE], sD2[2 * TILE], sD3[2 * TILE];
+  // per row of a step ([group][row]): -lse / scale, -delta, ordered-compare value
+  __shared__ __attribute__((aligned(16))) float sL0[2 * kRows], sL1[2 * kRows];
+  __shared__ __attribute__((aligned(16))) float sE0[2 * kRows], sE1[2 * kRows];
+  __shared__ __attribute__((aligned(16))) int sC0[2 * kRows], sC1[2 * kRows];
+  // A's packed probabilities for B ([wave pair][512 dwords])
+  __shared__ __attribute__((aligned(16))) uint32_t sP0[4 * 512], sP1[4 * 512];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int l32 = lane & 31, hi = lane >> 5;
+  const int gr = wave >> 2;                 // group
+  const int w4 = wave & 3;                  // wave within the group
+  const int gt = tid & 255;                 // thread within the group
+  const int half = w4 >> 1;                 // 32-key half of the tile
+  const int role = w4 & 1;                  // 0: A (S, P, dV), 1: B (dP, dS, dK)
+  const int pair = gr * 2 + half;
   const int G = a.Hq / a.Hkv;
 
-  // logical item: kv head major (its G heads share an XCD), key tiles from the
-  // first (most query tiles) to the last, then the head within the group
-  const int li = xcd_swizzle(blockIdx.x, a.Hkv * nkt * G);
-  const int g = li / (nkt * G);
-  const int rem = li % (nkt * G);
-  const int kt = kt0 + rem / G;
-  const int hh = rem % G;
-  const int h = g * G + hh;
+  // item: kv head major (its key tiles share an XCD), key tiles in order (the
+  // first ones have the longest query lists)
+  const int li = xcd_swizzle(blockIdx.x, a.Hkv * nkh);
+  const int g = li / nkh;
+  const int kh = kh0 + li % nkh;
+  const int kt = (kh * kKeys) / kBlock;     // block-mask key tile
 
-  const int key = kt * kBlock + wave * 32 + l32;
+  const int key = kh * kKeys + half * 32 + l32;
   const int kr = min(key, a.L - 1);
-  const int kw = key_w(a.code, key, a.P, a.L);
+  const int kw = min(key_w(a.code, key, a.P, a.L), kVRegular);
 
-  bf16x8 kf[KS], vf[KS];
+  // the wave's key operands: K for A, V for B (8 dims of key l32 per k-step)
+  bf16x8 kv[KS];
   {
-    const T *kp = reinterpret_cast<const T *>(a.k) + g * a.k_sh + (int64_t)kr * a.k_ss;
-    const T *vp = reinterpret_cast<const T *>(a.v) + g * a.v_sh + (int64_t)kr * a.v_ss;
+    const T *src = role == 0 ? reinterpret_cast<const T *>(a.k) + g * a.k_sh + (int64_t)kr * a.k_ss
+                             : reinterpret_cast<const T *>(a.v) + g * a.v_sh + (int64_t)kr * a.v_ss;
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      kf[ks] = load8(kp + ks * 16 + hi * 8);
-      vf[ks] = load8(vp + ks * 16 + hi * 8);
-    }
+    for (int ks = 0; ks < KS; ++ks) kv[ks] = load8(src + ks * 16 + hi * 8);
   }
 
-  const T *qp = reinterpret_cast<const T *>(a.q) + h * a.q_sh;
-  const T *dop = reinterpret_cast<const T *>(a.dout) + h * a.do_sh;
   TileList tiles = tile_list(a.q_num, a.q_idx, a.fq_num, a.fq_idx, kt, a.nQ);
   const int npart = tiles.npart;
-  const int ntot = tiles.ntot;
-  const int nstep = 2 * ntot;
-  auto step_base = [&](int j) { return tiles.at(j >> 1) * kBlock + (j & 1) * kQStep; };
+  const int npairs = G * tiles.ntot;                  // (query tile, head) pairs
+  const int mine = (npairs - gr + 1) / 2;              // pairs gr, gr + 2, ...
+  const int nsteps = 4 * mine;
+  const int nsteps_other = 4 * ((npairs - (1 - gr) + 1) / 2);
+  const int niter = (max(nsteps, nsteps_other) + 1 + 3) / 4 * 4;   // + 1: B's last dK step
 
-  // Q / dO operand of k-step ks for 32-row block qb: row qb * 32 + l32,
-  // granule (2 ks + hi) ^ swz(l32), i.e. byte offset qrow ^ (ks << 5);
-  // Q^T and dO^T through the transpose reads
-  const uint32_t qrow = opaque_u32((uint32_t)(l32 * HD + (((uint32_t)hi ^ swz<HD>(l32)) << 3)) * 2u);
+  auto info_of = [&](int j) -> StepInfo {
+    StepInfo s{0, 0, 0};
+    if (j < nsteps) {
+      const int i = gr + 2 * (j >> 2);
+      const int it = i / G;
+      s.h = g * G + i % G;
+      s.q0 = tiles.at(it) * kBlock + (j & 3) * kRows;
+      s.flags = (s.q0 < a.S ? 1 : 0) | (it < npart ? 2 : 0);
+    }
+    return s;
+  };
+
+  // Q / dO operand of k-step ks: row l32, granule (2 ks + hi) ^ swz(l32)
+  // LDS byte offsets, the group's block folded in so that every buffer base
+  // is an immediate: Q / dO operand of k-step ks (row l32, granule
+  // (2 ks + hi) ^ swz(l32)), the transposed operands, this lane's row data and
+  // its pair's P words
+  const uint32_t gofs = (uint32_t)(gr * TILE * 2);
+  const uint32_t qrow = (uint32_t)(l32 * HD + (((uint32_t)hi ^ swz<HD>(l32)) << 3)) * 2u;
+  uint32_t qk[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) qk[ks] = opaque_u32(gofs + (qrow ^ (uint32_t)(ks << 5)));
   TrOffsets<HD> tro;
   tro.init(lane);
+#pragma unroll
+  for (int sx = 0; sx < 2; ++sx)
+#pragma unroll
+    for (int mb = 0; mb < DB; ++mb) tro.off[sx][mb] = opaque_u32(tro.off[sx][mb] + gofs);
+  const uint32_t rofs = opaque_u32((uint32_t)(gr * kRows + 4 * hi) * 4u);
+  const uint32_t pofs = opaque_u32((uint32_t)(pair * 2048 + lane * 16));
   const float c = a.scale_log2;
+  const float inv_scale = 1.f / a.scale;
 
-  constexpr bool kDirect = sizeof(T) == 2;
-  TileStage<HD, kDirect ? 0 : kQStep, T> stQ, stD;
-  // per query row of the next step: raw lse, delta and code, converted at
-  // store time (converting here would wait for the tile loads in flight)
+  // tiles: global -> LDS two steps ahead (fp32: through one of two register
+  // slots); row data: global -> registers at the start of the step before
+  // its own, -> LDS at that step's end
+  GroupTile<HD, T> stQ[2], stD[2];
   float rl = 0.f, re = 0.f;
   int rc = kCodePad, rq = 0;
-  auto load_step = [&](int j, bf16_t *dQ, bf16_t *dD) {
-    const int q0 = step_base(j);
-    if constexpr (kDirect) {
-      tile_dma<HD, kQStep>(dQ, reinterpret_cast<const bf16_t *>(qp), a.q_ss, q0, a.S - 1);
-      tile_dma<HD, kQStep>(dD, reinterpret_cast<const bf16_t *>(dop), a.do_ss, q0, a.S - 1);
-    } else {
-      stQ.load(qp, a.q_ss, q0, a.S - 1);
-      stD.load(dop, a.do_ss, q0, a.S - 1);
+  auto load_tiles = [&](const StepInfo &s, bf16_t *dQ, bf16_t *dD, int slot) {
+    if (s.flags & 1) {
+      const T *qp = reinterpret_cast<const T *>(a.q) + s.h * a.q_sh;
+      const T *dop = reinterpret_cast<const T *>(a.dout) + s.h * a.do_sh;
+      stQ[slot].load(dQ, qp, a.q_ss, s.q0, a.S - 1, w4, gt);
+      stD[slot].load(dD, dop, a.do_ss, s.q0, a.S - 1, w4, gt);
     }
-    if (tid < kQStep) {
-      rq = q0 + tid;
+  };
+  auto store_tiles = [&](const StepInfo &s, bf16_t *dQ, bf16_t *dD, int slot) {
+    if (s.flags & 1) {
+      stQ[slot].store(dQ, gt);
+      stD[slot].store(dD, gt);
+    }
+  };
+  auto load_rows = [&](const StepInfo &s) {
+    if ((s.flags & 1) && gt < kRows) {
+      rq = s.q0 + gt;
       if (rq < a.S) {
-        rl = a.lse[(int64_t)h * a.S + rq];
-        re = a.delta[(int64_t)h * a.S + rq];
+        rl = a.lse[(int64_t)s.h * a.S + rq];
+        re = a.delta[(int64_t)s.h * a.S + rq];
         rc = a.code[rq];
       }
     }
   };
-  auto store_step = [&](bf16_t *dQ, bf16_t *dD, float *dL, float *dE, int *dM, int *dC) {
-    if constexpr (!kDirect) {
-      stQ.store(dQ);
-      stD.store(dD);
-    } else {
-      __builtin_amdgcn_s_waitcnt(0);
-    }
-    if (tid < kQStep) {
+  auto store_rows = [&](const StepInfo &s, float *dL, float *dE, int *dC) {
+    if ((s.flags & 1) && gt < kRows) {
       const bool in = rq < a.S;
       const int code = in ? rc : kCodePad;
       const float lse = in ? rl : kNegInfK;
-      dL[tid] = lse == kNegInfK ? 0.f : lse * kLog2e;
-      dE[tid] = in ? re : 0.f;
-      dM[tid] = (code == kCodePad || lse == kNegInfK) ? -1 : rq + a.P;   // causal bound, -1: sees nothing
-      dC[tid] = query_v(code);
+      const bool none = code == kCodePad || lse == kNegInfK;   // the row sees no key
+      dL[gt] = none ? 0.f : -lse * inv_scale;
+      dE[gt] = in ? -re : 0.f;
+      dC[gt] = none ? kVPadQuery : (code == kCodeX ? kVRegular : code);
     }
   };
 
-  f32x16 dkacc[DB], dvacc[DB];
+  f32x16 acc[DB];                     // A: dV^T, B: dK^T (dims x keys)
 #pragma unroll
-  for (int db = 0; db < DB; ++db) { dkacc[db] = zero16(); dvacc[db] = zero16(); }
+  for (int db = 0; db < DB; ++db) acc[db] = zero16();
 
-  auto run_step = [&](auto bsel, int j) {
-    constexpr int B = decltype(bsel)::value;
-    bf16_t *tQ = B ? sQ1 : sQ0;
-    bf16_t *tD = B ? sD1 : sD0;
-    const float *tL = B ? sL1 : sL0;
-    const float *tE = B ? sE1 : sE0;
-    const int *tM = B ? sM1 : sM0;
-    const int *tC = B ? sC1 : sC0;
-    const int q0 = step_base(j);
-    const bool partial = (j >> 1) < npart;
-    if (j + 1 < nstep) load_step(j + 1, B ? sQ0 : sQ1, B ? sD0 : sD1);
+  // Inactive steps multiply stale staging contents by zero words: start every
+  // buffer at zero so that stale data is always finite (0 * NaN would not vanish).
+  {
+    const i32x4 z = {0, 0, 0, 0};
+    for (int i = tid; i < 2 * TILE / 8; i += kThreads) {
+      reinterpret_cast<i32x4 *>(sQ0)[i] = z; reinterpret_cast<i32x4 *>(sQ1)[i] = z;
+      reinterpret_cast<i32x4 *>(sQ2)[i] = z; reinterpret_cast<i32x4 *>(sQ3)[i] = z;
+      reinterpret_cast<i32x4 *>(sD0)[i] = z; reinterpret_cast<i32x4 *>(sD1)[i] = z;
+      reinterpret_cast<i32x4 *>(sD2)[i] = z; reinterpret_cast<i32x4 *>(sD3)[i] = z;
+    }
+    for (int i = tid; i < 2 * kRows; i += kThreads) {
+      sL0[i] = 0.f; sL1[i] = 0.f; sE0[i] = 0.f; sE1[i] = 0.f; sC0[i] = kVPadQuery; sC1[i] = kVPadQuery;
+    }
+    for (int i = tid; i < 4 * 512; i += kThreads) { sP0[i] = 0u; sP1[i] = 0u; }
+    __syncthreads();
+  }
 
-    // Program order is the schedule. A step is 4 blocks of 2 KS MFMAs:
-    //   0: S / dP of rows 0..31,  1: S / dP of rows 32..63 (+ softmax of 0..31),
-    //   2: dV / dK update of rows 0..31 (+ softmax of 32..63),  3: update of 32..63.
-    // Every LDS operand is read kAhead MFMAs before its use (a ring of
-    // registers) and a scheduling fence closes each MFMA slot, so the compiler
-    // neither hoists all reads nor leaves a read next to its use. MASKED: a
-    // partial tile (masking compiled in; a full tile's step has none).
-    auto body = [&](auto masked) {
-      constexpr bool MASKED = decltype(masked)::value;
-      constexpr int kMm = 2 * KS;          // MFMAs of one block
-      constexpr int kSlots = 4 * kMm;      // MFMAs of the step
-      constexpr int kAhead = 4;
-      f32x16 sacc[2], dpacc[2];
-      i32x4 pb[2][2], dsb[2][2];   // packed P and dS operands (16 rows each)
-      // operand of slot t
-      auto read_op = [&](int t) -> bf16x8 {
-        const int blk = t / kMm, i = t % kMm;
-        if (blk < 2) {   // i = 2 ks + (0: Q row, 1: dO row)
-          const uint32_t off = (qrow ^ (uint32_t)((i >> 1) << 5)) + (uint32_t)(blk * 32 * HD * 2);
-          return lds_read8(reinterpret_cast<const bf16_t *>(lds_at((i & 1) ? tD : tQ, off)));
-        }
-        const int qb = blk - 2, u = (i >> 1) / DB, db = (i >> 1) % DB;   // i = 2 (u DB + db) + (0: dO^T, 1: Q^T)
-        return tro.operand((i & 1) ? tQ : tD, qb * 32 + 16 * u, db);
-      };
-      auto mma = [&](int t, const bf16x8 &op) {
-        const int blk = t / kMm, i = t % kMm;
-        if (blk < 2) {
-          if (i & 1) dpacc[blk] = mfma32(op, vf[i >> 1], dpacc[blk]);
-          else sacc[blk] = mfma32(op, kf[i >> 1], sacc[blk]);
-        } else {
-          const int qb = blk - 2, u = (i >> 1) / DB, db = (i >> 1) % DB;
-          if (i & 1) dkacc[db] = mfma32(op, __builtin_bit_cast(bf16x8, dsb[qb][u]), dkacc[db]);
-          else dvacc[db] = mfma32(op, __builtin_bit_cast(bf16x8, pb[qb][u]), dvacc[db]);
-        }
-      };
-      // scores 2 t, 2 t + 1 of row block qb: P (masked to 0) and dS, packed
-      // straight into the operand words (the accumulators are only read)
-      auto soft_pair = [&](int qb, int t) {
-        const int r0 = 2 * t;
-        const int ql = qb * 32 + 8 * (r0 >> 2) + 4 * hi + (r0 & 3);
-        const float2 l2 = *reinterpret_cast<const float2 *>(&tL[ql]);
-        const float2 e2 = *reinterpret_cast<const float2 *>(&tE[ql]);
-        float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[qb][r0], c, -l2.x));
-        float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[qb][r0 + 1], c, -l2.y));
-        if constexpr (MASKED) {
-          const int2 m2 = *reinterpret_cast<const int2 *>(&tM[ql]);
-          const int2 c2 = *reinterpret_cast<const int2 *>(&tC[ql]);
-          p0 = ((key <= m2.x) & (kw >= c2.x)) ? p0 : 0.f;
-          p1 = ((key <= m2.y) & (kw >= c2.y)) ? p1 : 0.f;
-        }
-        pb[qb][t >> 2][t & 3] = (int)cvt2(p0, p1);
-        dsb[qb][t >> 2][t & 3] = (int)cvt2(p0 * (dpacc[qb][r0] - e2.x), p1 * (dpacc[qb][r0 + 1] - e2.y));
-      };
-#pragma unroll
-      for (int qb = 0; qb < 2; ++qb) {
-        sacc[qb] = zero16();
-        dpacc[qb] = zero16();
-      }
-      bf16x8 ring[kAhead];
-#pragma unroll
-      for (int t = 0; t < kAhead; ++t) ring[t] = read_op(t);
-#pragma unroll
-      for (int t = 0; t < kSlots; ++t) {
-        const bf16x8 op = ring[t % kAhead];
-        if (t + kAhead < kSlots) ring[t % kAhead] = read_op(t + kAhead);
-        mma(t, op);
-        // the softmax of a row block rides on the next block's MFMAs, one
-        // pair of scores every other slot (8 pairs per block)
-        const int blk = t / kMm, i = t % kMm;
-        if ((blk == 1 || blk == 2) && (i & 1) && (i >> 1) < 8) soft_pair(blk - 1, i >> 1);
-        if ((blk == 1 || blk == 2) && i == kMm - 1) {
-#pragma unroll
-          for (int pr = kMm / 2; pr < 8; ++pr) soft_pair(blk - 1, pr);   // HD = 64: the rest
-        }
-        __builtin_amdgcn_sched_barrier(0);
-      }
-    };
-    if (q0 < a.S) {
-      if (partial) body(std::true_type{});
-      else body(std::false_type{});
+  auto qb = [&](int i) -> bf16_t * { return i == 0 ? sQ0 : (i == 1 ? sQ1 : (i == 2 ? sQ2 : sQ3)); };
+  auto db_ = [&](int i) -> bf16_t * { return i == 0 ? sD0 : (i == 1 ? sD1 : (i == 2 ? sD2 : sD3)); };
+  auto lb = [&](int i) -> float * { return i == 0 ? sL0 : sL1; };
+  auto eb = [&](int i) -> float * { return i == 0 ? sE0 : sE1; };
+  auto cb = [&](int i) -> int * { return i == 0 ? sC0 : sC1; };
+  auto pbuf = [&](int i) -> uint32_t * { return i == 0 ? sP0 : sP1; };
+
+  // step j's information sits in ring[j % 4] from step j - 2 on
+  StepInfo ring[4] = {{0, 0, 0}, {0, 0, 0}, {0, 0, 0}, {0, 0, 0}};
+  ring[0] = info_of(0);
+  ring[1] = info_of(1);
+  load_rows(ring[0]);
+  load_tiles(ring[0], sQ0 + gr * TILE, sD0 + gr * TILE, 0);
+  __builtin_amdgcn_s_waitcnt(0);   // this thread's loads of step 0 landed
+  store_tiles(ring[0], sQ0 + gr * TILE, sD0 + gr * TILE, 0);
+  store_rows(ring[0], sL0 + gr * kRows, sE0 + gr * kRows, sC0 + gr * kRows);
+  load_tiles(ring[1], sQ1 + gr * TILE, sD1 + gr * TILE, 1);
+  __syncthreads();
+
+  // B: dP - delta of the current and the previous step, alternating by step parity
+  f32x16 dp2[2] = {zero16(), zero16()};
+
+  // One step of role R: compute step j from Q buffer J % 4, dO buffer J % 4
+  // and row buffer J % 2; B's dK of step j - 1 reads Q buffer (J + 3) % 4 and
+  // P buffer (J + 1) % 2. Step j + 2's tiles load into buffers (J + 2) % 4,
+  // step j + 1's row data into row buffer (J + 1) % 2. Both roles pass the
+  // same barrier once per step.
+  auto run_step = [&](auto rsel, auto jsel, int j) {
+    constexpr int R = decltype(rsel)::value;
+    constexpr int J = decltype(jsel)::value;
+    const bf16_t *tQ = qb(J % 4);
+    const bf16_t *tD = db_(J % 4);
+    const bf16_t *tQprev = qb((J + 3) % 4);
+    const StepInfo cur = ring[J % 4];
+    const StepInfo prev = ring[(J + 3) % 4];
+    const StepInfo nxt1 = ring[(J + 1) % 4];
+    const bool cur_on = j < nsteps && (cur.flags & 1);
+    const bool prev_on = j >= 1 && j - 1 < nsteps && (prev.flags & 1);
+
+    // row data of step j + 1 first: vmcnt retires in issue order, and the
+    // wait at the end of this step must not cover the tiles of step j + 2
+    if (j + 1 < nsteps) load_rows(nxt1);
+    StepInfo nxt2{0, 0, 0};
+    if (j + 2 < nsteps) {
+      nxt2 = info_of(j + 2);
+      load_tiles(nxt2, qb((J + 2) % 4) + gr * TILE, db_((J + 2) % 4) + gr * TILE, J % 2);
     }
 
-    if (j + 1 < nstep)
-      store_step(B ? sQ0 : sQ1, B ? sD0 : sD1, B ? sL0 : sL1, B ? sE0 : sE1, B ? sM0 : sM1,
-                 B ? sC0 : sC1);
+    // The products run on every step, inactive ones included (the operands are
+    // then stale buffer contents, in bounds): a conditional accumulator update
+    // makes the compiler copy the accumulators around the branch. An inactive
+    // step contributes nothing because its P / dS words are cleared.
+    if constexpr (R == 0) {
+      const int keep = cur_on ? -1 : 0;
+      // S - lse / scale = Q K^T + (-lse / scale); register r is row 8 (r / 4) + 4 hi + r % 4
+      f32x16 sc = rows16(lb(J % 2), rofs);
+      bf16x8 op = lds_read8(reinterpret_cast<const bf16_t *>(lds_at(tQ, qk[0])));
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        bf16x8 nx;
+        if (ks + 1 < KS) nx = lds_read8(reinterpret_cast<const bf16_t *>(lds_at(tQ, qk[ks + 1])));
+        sc = mfma32(op, kv[ks], sc);
+        if (ks + 1 < KS) op = nx;
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sc[r] = __builtin_amdgcn_exp2f(sc[r] * c);
+      if (cur.flags & 2) {
+        // a real branch: if-converted, full tiles would pay for the masking
+        asm volatile("");
+        const int thr = key - cur.q0 - a.P - 4 * hi;   // causal: row offset (without 4 hi) >= thr
+        const int *tc = cb(J % 2);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const i32x4 qv = *reinterpret_cast<const i32x4 *>(lds_at(tc, rofs + 32 * i));
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const bool ok = (8 * i + e >= thr) & (kw >= qv[e]);
+            sc[4 * i + e] = ok ? sc[4 * i + e] : 0.f;
+          }
+        }
+      }
+      i32x4 pw[2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) pw[u][t] = (int)cvt2(sc[8 * u + 2 * t], sc[8 * u + 2 * t + 1]) & keep;
+      char *pp = reinterpret_cast<char *>(pbuf(J % 2));
+      *reinterpret_cast<i32x4 *>(pp + pofs) = pw[0];
+      *reinterpret_cast<i32x4 *>(pp + pofs + 1024) = pw[1];
+      // dV^T += dO^T P (16-row slice u, 32-dim block db)
+#pragma unroll
+      for (int t = 0; t < 2 * DB; ++t)
+        acc[t % DB] = mfma32(tro.operand(tD, (t / DB) * 16, t % DB), __builtin_bit_cast(bf16x8, pw[t / DB]),
+                             acc[t % DB]);
+    } else {
+      f32x16 &dp = dp2[J % 2];
+      const f32x16 &dprev = dp2[(J + 1) % 2];
+      const int keep = prev_on ? -1 : 0;
+      // dS of the previous step from A's P: dK^T += Q^T dS
+      const char *pp = reinterpret_cast<const char *>(pbuf((J + 1) % 2));
+      const i32x4 pw0 = *reinterpret_cast<const i32x4 *>(pp + pofs);
+      const i32x4 pw1 = *reinterpret_cast<const i32x4 *>(pp + pofs + 1024);
+      const i32x4 pws[2] = {pw0, pw1};
+      i32x4 dsw[2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          // bit_cast of the element through a named scalar: bit_cast of a vector
+          // subscript reads the vector's first element instead
+          const int wd = pws[u][t];
+          const bf16x2 pr = __builtin_bit_cast(bf16x2, wd);
+          dsw[u][t] = (int)cvt2((float)pr[0] * dprev[8 * u + 2 * t], (float)pr[1] * dprev[8 * u + 2 * t + 1]) & keep;
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < 2 * DB; ++t)
+        acc[t % DB] = mfma32(tro.operand(tQprev, (t / DB) * 16, t % DB), __builtin_bit_cast(bf16x8, dsw[t / DB]),
+                             acc[t % DB]);
+      // dP - delta = dO V^T + (-delta)
+      dp = rows16(eb(J % 2), rofs);
+      bf16x8 op = lds_read8(reinterpret_cast<const bf16_t *>(lds_at(tD, qk[0])));
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        bf16x8 nx;
+        if (ks + 1 < KS) nx = lds_read8(reinterpret_cast<const bf16_t *>(lds_at(tD, qk[ks + 1])));
+        dp = mfma32(op, kv[ks], dp);
+        if (ks + 1 < KS) op = nx;
+      }
+    }
+
+    if (j + 1 < nsteps) {
+      // this thread's loads of step j + 1 landed (issued one step ago): wait
+      // for all but the tiles of step j + 2 just issued
+      if constexpr (sizeof(T) == 2) {
+        constexpr int n = 2 * GroupTile<HD, T>::kInst;
+        if (nxt2.flags & 1) __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8));
+        else __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));   // vmcnt(0)
+      }
+      store_tiles(nxt1, qb((J + 1) % 4) + gr * TILE, db_((J + 1) % 4) + gr * TILE, (J + 1) % 2);
+      store_rows(nxt1, lb((J + 1) % 2) + gr * kRows, eb((J + 1) % 2) + gr * kRows, cb((J + 1) % 2) + gr * kRows);
+    }
+    ring[(J + 2) % 4] = nxt2;
     __syncthreads();
   };
 
-  if (nstep > 0) {
-    load_step(0, sQ0, sD0);
-    store_step(sQ0, sD0, sL0, sE0, sM0, sC0);
+  // four steps per iteration with no exit in between: an exit inside the
+  // unrolled body (or a separate tail) makes every accumulator a join of
+  // several register sets, which no longer fit. The step count is rounded up
+  // to a multiple of four; the extra steps are inactive (their P / dS words
+  // are cleared).
+  auto main_loop = [&](auto rsel) {
+    for (int j = 0; j < niter; j += 4) {
+      run_step(rsel, std::integral_constant<int, 0>{}, j);
+      run_step(rsel, std::integral_constant<int, 1>{}, j + 1);
+      run_step(rsel, std::integral_constant<int, 2>{}, j + 2);
+      run_step(rsel, std::integral_constant<int, 3>{}, j + 3);
+    }
+  };
+  if (role == 0) main_loop(std::integral_constant<int, 0>{});
+  else main_loop(std::integral_constant<int, 1>{});
+
+  // ---- group 1 hands its accumulators to group 0 (the staging buffers are
+  // free after the last barrier): wave (half, role) of group 1 writes into
+  // buffer [half][role], 16 KB in quads of registers, lane-interleaved ----
+  float *x = reinterpret_cast<float *>(half == 0 ? (role == 0 ? sQ0 : sD0) : (role == 0 ? sQ1 : sD1));
+  if (gr == 1) {
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        f32x4 v = {acc[db][4 * q], acc[db][4 * q + 1], acc[db][4 * q + 2], acc[db][4 * q + 3]};
+        *reinterpret_cast<f32x4 *>(x + ((db * 4 + q) * 64 + lane) * 4) = v;
+      }
   }
   __syncthreads();
-  for (int j = 0; j < nstep; j += 2) {
-    run_step(std::integral_constant<int, 0>{}, j);
-    if (j + 1 < nstep) run_step(std::integral_constant<int, 1>{}, j + 1);
-  }
-
-  // ---- epilogue: lane = key, registers = dims 8 (r / 4) + 4 hi + r % 4 ---------
-  if (key >= a.grad_start && key < a.L) {
-    const int64_t row = key - a.grad_start;
-    if (G == 1) {
-      T *dkr = reinterpret_cast<T *>(a.dk) + g * a.dk_sh + row * a.dk_ss;
-      T *dvr = reinterpret_cast<T *>(a.dv) + g * a.dv_sh + row * a.dv_ss;
+  if (gr == 0) {
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const f32x4 v = *reinterpret_cast<const f32x4 *>(x + ((db * 4 + q) * 64 + lane) * 4);
+        acc[db][4 * q] += v[0]; acc[db][4 * q + 1] += v[1]; acc[db][4 * q + 2] += v[2]; acc[db][4 * q + 3] += v[3];
+      }
+    // lane = key, registers = dims 8 (r / 4) + 4 hi + r % 4 of block db
+    if (key >= a.grad_start && key < a.L) {
+      const int64_t row = key - a.grad_start;
+      const float f = role == 0 ? 1.f : a.scale;
+      T *out = role == 0 ? reinterpret_cast<T *>(a.dv) + g * a.dv_sh + row * a.dv_ss
+                         : reinterpret_cast<T *>(a.dk) + g * a.dk_sh + row * a.dk_ss;
 #pragma unroll
       for (int db = 0; db < DB; ++db)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int d0 = db * 32 + 8 * i + 4 * hi;
-          const f32x16 &ck = dkacc[db];
-          const f32x16 &cv = dvacc[db];
-          store4(dkr + d0, ck[4 * i] * a.scale, ck[4 * i + 1] * a.scale, ck[4 * i + 2] * a.scale,
-                 ck[4 * i + 3] * a.scale);
-          store4(dvr + d0, cv[4 * i], cv[4 * i + 1], cv[4 * i + 2], cv[4 * i + 3]);
-        }
-    } else {
-      // partial of head hh: ws[tensor][hh][row][g][d] (fp32)
-      const int64_t Lg = a.L - a.grad_start;
-      const int64_t plane = Lg * a.Hkv * HD;
-      float *pk = a.dkv_ws + (int64_t)hh * plane + (row * a.Hkv + g) * HD;
-      float *pv = pk + (int64_t)G * plane;
-#pragma unroll
-      for (int db = 0; db < DB; ++db)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int d0 = db * 32 + 8 * i + 4 * hi;
-          const f32x16 &ck = dkacc[db];
-          const f32x16 &cv = dvacc[db];
-          store4(pk + d0, ck[4 * i] * a.scale, ck[4 * i + 1] * a.scale, ck[4 * i + 2] * a.scale,
-                 ck[4 * i + 3] * a.scale);
-          store4(pv + d0, cv[4 * i], cv[4 * i + 1], cv[4 * i + 2], cv[4 * i + 3]);
-        }
+        for (int i = 0; i < 4; ++i)
+          store4(out + db * 32 + 8 * i + 4 * hi, acc[db][4 * i] * f, acc[db][4 * i + 1] * f,
+                 acc[db][4 * i + 2] * f, acc[db][4 * i + 3] * f);
     }
   }
-}
-
-// dk[row, g, :] = sum_hh ws_k[hh, row, g, :] (and dv), hh ascending. One thread
-// per 4 consecutive values of one (tensor, row, g).
-template <int HD, typename T>
-__global__ __launch_bounds__(256) void dkdv_reduce_kernel(AttnArgs a) {
-  const int64_t Lg = a.L - a.grad_start;
-  const int64_t plane = Lg * a.Hkv * HD;
-  const int64_t n4 = plane / 4;
-  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int G = a.Hq / a.Hkv;
-  if (t >= 2 * n4) return;
-  const int tensor = t >= n4;
-  const int64_t e = (t - tensor * n4) * 4;       // element offset in one plane
-  const float *src = a.dkv_ws + (int64_t)tensor * G * plane + e;
-  f32x4 acc = *reinterpret_cast<const f32x4 *>(src);
-  for (int hh = 1; hh < G; ++hh) {
-    const f32x4 x = *reinterpret_cast<const f32x4 *>(src + hh * plane);
-    acc[0] += x[0]; acc[1] += x[1]; acc[2] += x[2]; acc[3] += x[3];
-  }
-  const int64_t row = e / (a.Hkv * HD);
-  const int g = (int)((e / HD) % a.Hkv);
-  const int d = (int)(e % HD);
-  T *dst = tensor ? reinterpret_cast<T *>(a.dv) + g * a.dv_sh + row * a.dv_ss
-                  : reinterpret_cast<T *>(a.dk) + g * a.dk_sh + row * a.dk_ss;
-  store4(dst + d, acc[0], acc[1], acc[2], acc[3]);
 }
 
 template <int HD, typename T>
 void dkdv_launch(const AttnArgs &a, hipStream_t st) {
-  const int kt0 = a.grad_start / kBlock;
-  const int nkt = a.nKV - kt0;
-  if (nkt <= 0 || a.grad_start >= a.L) return;
-  const int G = a.Hq / a.Hkv;
-  hipLaunchKernelGGL((attn_bwd_dkdv_kernel<HD, T>), dim3(a.Hkv * nkt * G), dim3(256), 0, st, a, kt0, nkt);
-  if (G > 1) {
-    const int64_t n = 2 * (int64_t)(a.L - a.grad_start) * a.Hkv * HD / 4;
-    hipLaunchKernelGGL((dkdv_reduce_kernel<HD, T>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, a);
-  }
+  if (a.grad_start >= a.L) return;
+  const int kh0 = a.grad_start / kKeys;
+  const int nkh = (a.L - kh0 * kKeys + kKeys - 1) / kKeys;
+  hipLaunchKernelGGL((attn_bwd_dkdv_kernel<HD, T>), dim3(a.Hkv * nkh), dim3(kThreads), 0, st, a, kh0, nkh);
 }
 
 template <int HD, typename T>

@@ -158,7 +158,7 @@ int mga_attn_fwd(const void *q, int64_t q_sh, int64_t q_ss, const void *k, int64
 int mga_attn_bwd(const void *q, int64_t q_sh, int64_t q_ss, const void *k, int64_t k_sh,
                  int64_t k_ss, const void *v, int64_t v_sh, int64_t v_ss, const void *o,
                  int64_t o_sh, int64_t o_ss, const void *dout, int64_t do_sh, int64_t do_ss,
-                 const float *lse, float *delta, float *dkv_ws, void *dq, int64_t dq_sh, int64_t dq_ss, void *dk,
+                 const float *lse, float *delta, void *dq, int64_t dq_sh, int64_t dq_ss, void *dk,
                  int64_t dk_sh, int64_t dk_ss, void *dv, int64_t dv_sh, int64_t dv_ss,
                  int32_t grad_start, const int32_t *code, const int32_t *kv_num,
                  const int32_t *kv_idx, const int32_t *full_kv_num, const int32_t *full_kv_idx,
@@ -182,8 +182,6 @@ int mga_attn_bwd(const void *q, int64_t q_sh, int64_t q_ss, const void *k, int64
   if ((passes & MGA_BWD_DKDV) && grad_start < L) {
     if ((rc = check_operand("dk", dk, dk_sh, dk_ss, eb))) return rc;
     if ((rc = check_operand("dv", dv, dv_sh, dv_ss, eb))) return rc;
-    if (Hq != Hkv && (!dkv_ws || !aligned16(dkv_ws)))
-      return fail(MGA_ERR_INVALID, "mga_attn_bwd: dkv_ws (2*G*(L-grad_start)*Hkv*head_dim floats, 16-byte aligned) is required when Hq > Hkv");
   }
   if (!lse || !delta || !code || !kv_num || !kv_idx || !full_kv_num || !full_kv_idx || !q_num ||
       !q_idx || !full_q_num || !full_q_idx)
@@ -194,7 +192,7 @@ int mga_attn_bwd(const void *q, int64_t q_sh, int64_t q_ss, const void *k, int64
   a.v = v; a.v_sh = v_sh; a.v_ss = v_ss;
   a.o = o; a.o_sh = o_sh; a.o_ss = o_ss;
   a.dout = dout; a.do_sh = do_sh; a.do_ss = do_ss;
-  a.lse = const_cast<float *>(lse); a.delta = delta; a.dkv_ws = dkv_ws;
+  a.lse = const_cast<float *>(lse); a.delta = delta;
   a.dq = dq; a.dq_sh = dq_sh; a.dq_ss = dq_ss;
   a.dk = dk; a.dk_sh = dk_sh; a.dk_ss = dk_ss;
   a.dv = dv; a.dv_sh = dv_sh; a.dv_ss = dv_ss;

@@ -14,7 +14,6 @@ struct AttnArgs {
   const void *dout; int64_t do_sh, do_ss;
   float *lse;                               // [Hq, S] natural log
   float *delta;                             // [Hq, S] workspace (bwd)
-  float *dkv_ws;                            // [2, G, L - grad_start, Hkv, D] fp32 partials (bwd, G > 1)
   void *dq; int64_t dq_sh, dq_ss;
   void *dk; int64_t dk_sh, dk_ss;
   void *dv; int64_t dv_sh, dv_ss;

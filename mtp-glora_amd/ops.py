@@ -179,19 +179,16 @@ def attn_fwd(q, k, v, code, bm: dict, P: int, scale: float):
 
 def bwd_buffers(q, k, grad_start: int) -> dict:
     """Output and workspace buffers of ``attn_bwd``: dq [1, S, Hq, D], dk/dv
-    [1, L - grad_start, Hkv, D] (None when grad_start == L), delta [Hq * S] fp32
-    and the fp32 dK/dV partials of the G query heads per kv head (G > 1)."""
+    [1, L - grad_start, Hkv, D] (None when grad_start == L) and delta
+    [Hq * S] fp32."""
     _, Hq, S, D = q.shape
     _, Hkv, L, _ = k.shape
     dev, dt = q.device, q.dtype
     Lg = L - grad_start
-    G = Hq // Hkv
     return dict(dq=torch.empty(1, S, Hq, D, dtype=dt, device=dev),
                 dk=torch.empty(1, Lg, Hkv, D, dtype=dt, device=dev) if Lg > 0 else None,
                 dv=torch.empty(1, Lg, Hkv, D, dtype=dt, device=dev) if Lg > 0 else None,
-                delta=torch.empty(Hq * S, dtype=torch.float32, device=dev),
-                dkv_ws=(torch.empty(2 * G * Lg * Hkv * D, dtype=torch.float32, device=dev)
-                        if Lg > 0 and G > 1 else None))
+                delta=torch.empty(Hq * S, dtype=torch.float32, device=dev))
 
 
 def attn_bwd(q, k, v, o, lse, dout, code, bm: dict, P: int, scale: float, grad_start: int,
@@ -224,12 +221,10 @@ def attn_bwd(q, k, v, o, lse, dout, code, bm: dict, P: int, scale: float, grad_s
         raise ValueError("backward buffers do not match the operands")
     dk_ptr = dk.data_ptr() if dk is not None else None
     dv_ptr = dv.data_ptr() if dv is not None else None
-    ws = b.get("dkv_ws")
-    ws_ptr = ws.data_ptr() if ws is not None else None
     # o3 is [S, Hq, D]: element (h, s, d) at h * D + s * Hq * D + d
     _lib.call("mga_attn_bwd", qq.data_ptr(), q_sh, q_ss, kk.data_ptr(), k_sh, k_ss,
               vv.data_ptr(), v_sh, v_ss, o3.data_ptr(), o3.stride(1), o3.stride(0),
-              d3.data_ptr(), d3.stride(1), d3.stride(0), lse.data_ptr(), delta.data_ptr(), ws_ptr,
+              d3.data_ptr(), d3.stride(1), d3.stride(0), lse.data_ptr(), delta.data_ptr(),
               dq.data_ptr(), D, Hq * D, dk_ptr, D, Hkv * D, dv_ptr, D, Hkv * D,
               int(grad_start), code.data_ptr(),
               bm["kv_num_blocks"].data_ptr(), bm["kv_indices"].data_ptr(),
