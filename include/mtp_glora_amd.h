@@ -6,7 +6,9 @@
  * enqueues its kernels on `stream` (a hipStream_t, NULL = default stream) and
  * returns MGA_OK or an error code; mga_last_error() gives the message of the
  * last failure on the calling thread. Nothing here allocates device memory:
- * callers own every buffer (outputs and workspaces included).
+ * callers own every buffer (outputs and workspaces included); the one device
+ * array the library holds itself is the fixed workspace of
+ * mga_attn_bwd_noalloc, created with the library's code object.
  *
  * Layout conventions (batch size 1, as the reference assumes everywhere,
  * mtp_glora/data_utils/collator.py:123-124, 242-243, 308-309):
@@ -153,6 +155,37 @@ int mga_attn_bwd(const void *q, int64_t q_sh, int64_t q_ss,
                  const int32_t *full_q_num, const int32_t *full_q_idx,
                  int32_t S, int32_t L, int32_t P, int32_t Hq, int32_t Hkv,
                  int32_t head_dim, int32_t dtype, float scale, int32_t passes, void *stream);
+
+/*
+ * mga_attn_bwd without the delta workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). No counterpart in the reference. delta
+ * lives in a fixed device array of 2 097 152 floats (8 MiB) that the library
+ * holds on every GPU it runs on until the process ends; calls with
+ * Hq * S > 2 097 152 are rejected with MGA_ERR_INVALID before any device work.
+ * The call itself allocates nothing (no hipMalloc, no library allocation).
+ * Every call on a GPU shares that GPU's array and it keeps the last call's
+ * contents: calls that overlap on one GPU (e.g. on two streams) race, and an
+ * MGA_BWD_DKDV-only call reads the delta the last MGA_BWD_DQ call on that GPU
+ * wrote. The calling thread's current device must be the stream's device.
+ * Results are bit-for-bit those of mga_attn_bwd.
+ */
+int mga_attn_bwd_noalloc(const void *q, int64_t q_sh, int64_t q_ss,
+                         const void *k, int64_t k_sh, int64_t k_ss,
+                         const void *v, int64_t v_sh, int64_t v_ss,
+                         const void *o, int64_t o_sh, int64_t o_ss,
+                         const void *dout, int64_t do_sh, int64_t do_ss,
+                         const float *lse,
+                         void *dq, int64_t dq_sh, int64_t dq_ss,
+                         void *dk, int64_t dk_sh, int64_t dk_ss,
+                         void *dv, int64_t dv_sh, int64_t dv_ss,
+                         int32_t grad_start, const int32_t *code,
+                         const int32_t *kv_num, const int32_t *kv_idx,
+                         const int32_t *full_kv_num, const int32_t *full_kv_idx,
+                         const int32_t *q_num, const int32_t *q_idx,
+                         const int32_t *full_q_num, const int32_t *full_q_idx,
+                         int32_t S, int32_t L, int32_t P, int32_t Hq, int32_t Hkv,
+                         int32_t head_dim, int32_t dtype, float scale, int32_t passes, void *stream);
 
 /*
  * Qwen3 query / key normalisation and rotary embedding, fused:

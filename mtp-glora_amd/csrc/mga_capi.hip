@@ -4,6 +4,8 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <mutex>
+
 #include "../../include/mtp_glora_amd.h"
 #include "mga_common.hpp"
 #include "mga_internal.hpp"
@@ -56,6 +58,36 @@ int check_attn_common(int32_t S, int32_t L, int32_t P, int32_t Hq, int32_t Hkv, 
   if (Hq <= 0 || Hkv <= 0 || Hq % Hkv) return fail(MGA_ERR_INVALID, "Hq (%d) must be a positive multiple of Hkv (%d)", Hq, Hkv);
   if (hd != 64 && hd != 128) return fail(MGA_ERR_INVALID, "head_dim must be 64 or 128 (got %d)", hd);
   if (!elem_bytes(dtype)) return fail(MGA_ERR_INVALID, "unknown dtype code %d", dtype);
+  return MGA_OK;
+}
+
+// Workspace of mga_attn_bwd_noalloc (delta = rowsum(o * dout) per query head
+// and row): a device array of kNoAllocDeltaFloats floats, one copy on every GPU
+// the library runs on, held until the process ends. Host code reaches it only
+// through the address hipGetSymbolAddress returns for the current device.
+constexpr int64_t kNoAllocDeltaFloats = int64_t(1) << 21;   // 8 MiB: Hq * S <= 2 097 152
+static __device__ __align__(256) float scratch[kNoAllocDeltaFloats];
+
+std::mutex g_scratch_mu;
+constexpr int kMaxDevices = 256;
+float *g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's copy of scratch, looked up once per device.
+int scratch_for_current_device(float **out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(MGA_ERR_HIP, "mga_attn_bwd_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(MGA_ERR_INVALID, "mga_attn_bwd_noalloc: device id %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    float *ptr = nullptr;
+    e = hipGetSymbolAddress((void **)&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+      return fail(MGA_ERR_HIP, "mga_attn_bwd_noalloc: hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                  hipGetErrorString(e));
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
   return MGA_OK;
 }
 
@@ -206,6 +238,32 @@ int mga_attn_bwd(const void *q, int64_t q_sh, int64_t q_ss, const void *k, int64
   a.scale_log2 = scale * mga::kLog2e;
   mga::launch_attn_bwd(a, head_dim, dtype == MGA_DTYPE_F32, passes, (hipStream_t)stream);
   return check_launch("mga_attn_bwd");
+}
+
+int mga_attn_bwd_noalloc(const void *q, int64_t q_sh, int64_t q_ss, const void *k, int64_t k_sh,
+                         int64_t k_ss, const void *v, int64_t v_sh, int64_t v_ss, const void *o,
+                         int64_t o_sh, int64_t o_ss, const void *dout, int64_t do_sh, int64_t do_ss,
+                         const float *lse, void *dq, int64_t dq_sh, int64_t dq_ss, void *dk,
+                         int64_t dk_sh, int64_t dk_ss, void *dv, int64_t dv_sh, int64_t dv_ss,
+                         int32_t grad_start, const int32_t *code, const int32_t *kv_num,
+                         const int32_t *kv_idx, const int32_t *full_kv_num, const int32_t *full_kv_idx,
+                         const int32_t *q_num, const int32_t *q_idx, const int32_t *full_q_num,
+                         const int32_t *full_q_idx, int32_t S, int32_t L, int32_t P, int32_t Hq,
+                         int32_t Hkv, int32_t head_dim, int32_t dtype, float scale, int32_t passes,
+                         void *stream) {
+  if (Hq <= 0 || S <= 0) return fail(MGA_ERR_INVALID, "mga_attn_bwd_noalloc: Hq (%d) and S (%d) must be positive", Hq, S);
+  if ((int64_t)Hq * S > kNoAllocDeltaFloats)
+    return fail(MGA_ERR_INVALID,
+                "mga_attn_bwd_noalloc: Hq * S = %lld exceeds its fixed workspace of %lld (query head, row) "
+                "pairs; use mga_attn_bwd with a caller-allocated delta",
+                (long long)Hq * S, (long long)kNoAllocDeltaFloats);
+  float *delta = nullptr;
+  int rc = scratch_for_current_device(&delta);
+  if (rc != MGA_OK) return rc;
+  return mga_attn_bwd(q, q_sh, q_ss, k, k_sh, k_ss, v, v_sh, v_ss, o, o_sh, o_ss, dout, do_sh, do_ss, lse,
+                      delta, dq, dq_sh, dq_ss, dk, dk_sh, dk_ss, dv, dv_sh, dv_ss, grad_start, code, kv_num,
+                      kv_idx, full_kv_num, full_kv_idx, q_num, q_idx, full_q_num, full_q_idx, S, L, P, Hq,
+                      Hkv, head_dim, dtype, scale, passes, stream);
 }
 
 namespace {

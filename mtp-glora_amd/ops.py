@@ -192,14 +192,18 @@ def bwd_buffers(q, k, grad_start: int) -> dict:
 
 
 def attn_bwd(q, k, v, o, lse, dout, code, bm: dict, P: int, scale: float, grad_start: int,
-             passes: int = _lib.BWD_DQ | _lib.BWD_DKDV, buffers: dict | None = None):
+             passes: int = _lib.BWD_DQ | _lib.BWD_DKDV, buffers: dict | None = None,
+             no_alloc: bool = False):
     """Gradients of ``attn_fwd``. Returns dq [1, Hq, S, D] (a transposed view of
     an [1, S, Hq, D] buffer), and dk, dv [1, Hkv, L - grad_start, D] (views of
     [1, L - grad_start, Hkv, D] buffers) or None when grad_start == L.
 
     ``passes`` selects the dQ pass (which also writes delta = rowsum(o * dout))
     and/or the dK/dV pass; to issue them as two calls in stream order, pass the
-    same ``buffers`` (from ``bwd_buffers``) to both, the dQ pass first."""
+    same ``buffers`` (from ``bwd_buffers``) to both, the dQ pass first.
+
+    ``no_alloc`` calls ``mga_attn_bwd_noalloc``: delta lives in the library's
+    fixed per-GPU workspace instead of ``buffers["delta"]``."""
     qq, q_sh, q_ss = _rows("query", q)
     kk, k_sh, k_ss = _rows("key", k)
     vv, v_sh, v_ss = _rows("value", v)
@@ -222,9 +226,13 @@ def attn_bwd(q, k, v, o, lse, dout, code, bm: dict, P: int, scale: float, grad_s
     dk_ptr = dk.data_ptr() if dk is not None else None
     dv_ptr = dv.data_ptr() if dv is not None else None
     # o3 is [S, Hq, D]: element (h, s, d) at h * D + s * Hq * D + d
-    _lib.call("mga_attn_bwd", qq.data_ptr(), q_sh, q_ss, kk.data_ptr(), k_sh, k_ss,
-              vv.data_ptr(), v_sh, v_ss, o3.data_ptr(), o3.stride(1), o3.stride(0),
-              d3.data_ptr(), d3.stride(1), d3.stride(0), lse.data_ptr(), delta.data_ptr(),
+    head = (["mga_attn_bwd_noalloc", qq.data_ptr(), q_sh, q_ss, kk.data_ptr(), k_sh, k_ss,
+             vv.data_ptr(), v_sh, v_ss, o3.data_ptr(), o3.stride(1), o3.stride(0),
+             d3.data_ptr(), d3.stride(1), d3.stride(0), lse.data_ptr()] if no_alloc else
+            ["mga_attn_bwd", qq.data_ptr(), q_sh, q_ss, kk.data_ptr(), k_sh, k_ss,
+             vv.data_ptr(), v_sh, v_ss, o3.data_ptr(), o3.stride(1), o3.stride(0),
+             d3.data_ptr(), d3.stride(1), d3.stride(0), lse.data_ptr(), delta.data_ptr()])
+    _lib.call(*head,
               dq.data_ptr(), D, Hq * D, dk_ptr, D, Hkv * D, dv_ptr, D, Hkv * D,
               int(grad_start), code.data_ptr(),
               bm["kv_num_blocks"].data_ptr(), bm["kv_indices"].data_ptr(),

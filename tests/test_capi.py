@@ -83,3 +83,14 @@ def test_attention_invalid_arguments(mga):
 def test_python_errors_are_raised(mga):
     with pytest.raises(mga._lib.CapacityError):
         mga._lib.call("mga_kv_append", 16, 16, 1024, 128, 8, None, 4, 16, 16, 1024, 128, 6, 8, 2, 128, 0, None)
+
+
+def test_noalloc_rejects_oversized_calls_before_device_work(mga):
+    """Hq * S above mga_attn_bwd_noalloc's fixed workspace is rejected before
+    the library touches a device."""
+    lib = mga.load_library()
+    P = ctypes.c_void_p(16)
+    rc = lib.mga_attn_bwd_noalloc(P, 128, 4096, P, 128, 128, P, 128, 128, P, 128, 4096, P, 128, 4096, P,
+                                  P, 128, 4096, P, 128, 1024, P, 128, 1024, 0, P, P, P, P, P, P, P, P, P,
+                                  1 << 20, 1 << 20, 0, 32, 8, 128, 0, 0.1, 3, None)
+    assert rc == mga._lib.MGA_ERR_INVALID and b"workspace" in lib.mga_last_error()
