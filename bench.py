@@ -360,6 +360,77 @@ PHASE_KERNEL = {"fwd": "attn_fwd_kernel", "bwd_dq_pass": "attn_bwd_dq_kernel",
 CALIB_ROWS = 65536   # rows per head of the calibration copy (8 heads x 256 B x 2 tensors = 268 MB)
 
 
+def load_mfma(path: str) -> dict:
+    """Per attention kernel: MFMA-busy fraction and the MFMA work the counters
+    saw over the credited work, from a committed counter summary
+    (rocprof_summary.py mfma), or {}."""
+    try:
+        with open(path) as f:
+            t = json.load(f)
+    except (OSError, ValueError):
+        return {}
+    out = {}
+    for k, e in t.get("kernels", {}).items():
+        out[k] = {n: round(e[n], 4) for n in ("mfma_busy_frac", "mfma_flop_over_credited", "valu_per_mfma",
+                                             "salu_per_mfma", "lds_per_mfma") if n in e}
+    return out
+
+
+def north_star_phase(torch, mga, syn, steps: int, warmup: int) -> dict:
+    """The north-star point: one Qwen3-8B layer-chunk of 4096 regular rows plus
+    512 anchors x 4 mask rows (S = 6144) against a 28 672-token cached prefix
+    (config 3's last chunk), timed as the main step is: block mask, staging
+    append, attention forward and backward, regular-row commit."""
+    dev = torch.device("cuda:0")
+    Hq, Hkv, D, P, n_reg, n_anchor, draft = 32, 8, 128, 28672, 4096, 512, 4
+    anchors = syn.sample_anchors(n_reg, n_anchor, SEED + 7)
+    chunk0 = syn.mtp_chunk(n_reg, anchors, draft, pos0=P, device=dev, seed=SEED + 7)
+    S = chunk0["gate_mask"].shape[1]
+    L = P + S
+    scale = D ** -0.5
+    gens = [torch.Generator(device=dev).manual_seed(SEED + 70 + i) for i in range(6)]
+    rnd = lambda shape, g, sd: (torch.randn(*shape, generator=g, device=dev) * sd).bfloat16()
+    q = rnd((1, S, Hq, D), gens[0], 0.5).transpose(1, 2).requires_grad_()
+    k = rnd((1, S, Hkv, D), gens[1], 0.5).transpose(1, 2).requires_grad_()
+    v = rnd((1, S, Hkv, D), gens[2], 0.5).transpose(1, 2).requires_grad_()
+    do = rnd((1, S, Hq, D), gens[5], 1.0)
+    mgr = mga.StreamingKVCacheManager(capacity=L + 256, sanity_check=False)
+    cache = mgr.new_cache(num_layers=1)
+    cache.append_prefix([rnd((1, Hkv, P, D), gens[3], 0.5)], [rnd((1, Hkv, P, D), gens[4], 0.5)])
+    mgr.past_seen_tokens = P
+    module = torch.nn.Module()
+
+    def step():
+        chunk = mgr.prepare_data_with_kv_cache(dict(chunk0))
+        kf, vf = cache.update(k, v, 0)
+        o, _ = mga.mtp_attention_forward(module, q, kf, vf, chunk["attention_mask"], scaling=scale)
+        grads = torch.autograd.grad(o, (q, k, v), do)
+        mgr.extract_regular_kv_cache_for_next_chunk(chunk, cache)
+        cache.crop(P)
+        mgr.past_seen_tokens = P
+        return grads
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    bm = mga.build_mtp_block_mask(chunk0["gate_mask"], P)
+    a_pre, a_cur = tile_areas(bm, S, L, P)
+    fl = Hq * D * (4 * (a_pre + a_cur) + 6 * a_pre + 10 * a_cur)
+    tf = fl / (ms * 1e-3) / 1e12
+    return {"workload": "north-star point: Qwen3-8B layer-chunk, 4096 regular + 512x4 mask rows vs a "
+                        "28672-token prefix (config 3, last chunk)",
+            "chunk_rows": S, "prefix": P, "credited_gflop": round(fl / 1e9, 1), "ms_per_step": round(ms, 4),
+            "tflops": round(tf, 2), "frac": round(tf / PEAK_MFMA_BF16_TFLOPS, 4), "steps": steps,
+            "target_frac": 0.5}
+
+
 def load_traffic(path: str, config: int):
     """HBM bytes per launch per kernel from a committed counter summary
     (FETCH_SIZE + WRITE_SIZE scaled by the calibration copy), or None."""
@@ -530,6 +601,10 @@ def main() -> int:
                          "of each hot-path kernel; prints their byte counts and exits")
     ap.add_argument("--traffic", default=str(ROOT / "profiles" / "config2_traffic.json"),
                     help="counter summary (from rocprof_summary.py) that fills roofline.traffic")
+    ap.add_argument("--mfma", default=str(ROOT / "profiles" / "config2_mfma.json"),
+                    help="counter summary (rocprof_summary.py mfma) that fills roofline.mfma_busy")
+    ap.add_argument("--north-star-steps", type=int, default=10,
+                    help="timed steps of the north-star point (0 = skip)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -654,6 +729,7 @@ def main() -> int:
     qk_rope = qk_rope_phase(torch, timer, S, Hq, Hkv, D, n, cpu_tokens=256)
     lora = gated_lora_phase(torch, timer, S, Hq * D, (Hq + 2 * Hkv) * D, 96, 0.05, n, cpu_rows=32)
     traffic = load_traffic(args.traffic, args.config)
+    mfma = load_mfma(args.mfma) if args.config == 2 else {}
     credited = {"fwd": fl_fwd, "bwd_dq_pass": fl_dq, "bwd_dkdv_pass": fl_dkdv}
     dom = max(credited, key=lambda kname: phases[kname])
     attn_ms = t_fwd + t_dq + t_dkdv
@@ -679,7 +755,8 @@ def main() -> int:
         "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(dom_tflops, 2),
                      "peak": PEAK_MFMA_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(dom_tflops / PEAK_MFMA_BF16_TFLOPS, 4),
-                     "traffic": traffic.get(PHASE_KERNEL[dom]) if traffic else None},
+                     "traffic": traffic.get(PHASE_KERNEL[dom]) if traffic else None,
+                     "mfma_busy": mfma.get(PHASE_KERNEL[dom], {}).get("mfma_busy_frac")},
         "attention": {"credited_gflop": {"fwd": fl_fwd / 1e9, "bwd": (fl_dq + fl_dkdv) / 1e9,
                                          "total": fl_total / 1e9},
                       "tiles_area": {"prefix": a_pre, "chunk": a_cur},
@@ -687,6 +764,8 @@ def main() -> int:
                       "fwd_bwd_tflops": round(fl_total / (attn_ms * 1e-3) / 1e12, 2),
                       "fwd_bwd_frac": round(fl_total / (attn_ms * 1e-3) / 1e12 / PEAK_MFMA_BF16_TFLOPS, 4),
                       "fwd_tflops": round(fl_fwd / (t_fwd * 1e-3) / 1e12, 2),
+                      "mfma_counters": ({PHASE_KERNEL[k_]: mfma.get(PHASE_KERNEL[k_]) for k_ in credited}
+                                        if mfma else None),
                       "bwd_tflops": round((fl_dq + fl_dkdv) / ((t_dq + t_dkdv) * 1e-3) / 1e12, 2)},
         "append": {"bytes": append_bytes, "ms": round(t_commit, 5), "GBps": round(commit_gbps, 1),
                    "frac": round(commit_gbps / PEAK_HBM_GBPS, 4), "peak": PEAK_HBM_GBPS,
@@ -699,6 +778,8 @@ def main() -> int:
         "gated_lora_qkv": lora,
         "host_ms_per_step": round(host_ms, 4),
     }
+    if args.north_star_steps > 0:
+        out["north_star"] = north_star_phase(torch, mga, syn, args.north_star_steps, 3)
 
     if args.cpu_reps > 0:
         cb = cpu_baseline(cfg, chunk0["gate_mask"].cpu(), args.cpu_reps, args.cpu_heads)
@@ -708,8 +789,10 @@ def main() -> int:
             "value": round(cpu_tflops, 4), "unit": "TFLOP/s", "cores": cb["threads"], "kind": "port",
             "sample": (f"torch flex_attention eager (dense math path) fwd+bwd on CPU with the restated "
                        f"MTP mask_mod: {args.cpu_heads} query heads of one KV head at the full "
-                       f"S={S}, P+S={L}; median of {args.cpu_reps} runs after a warm-up; credited "
-                       f"FLOPs scaled by {args.cpu_heads}/{Hq}"),
+                       f"S={S}, P+S={L}; median of {args.cpu_reps} runs after a warm-up; value "
+                       f"extrapolated from this one of {Hq // args.cpu_heads} KV-head groups (credited "
+                       f"FLOPs of the sample = {args.cpu_heads}/{Hq} of the layer's)"),
+            "extrapolated": f"x{Hq // args.cpu_heads} (one KV-head group timed)",
             "seconds": round(cb["seconds"], 3), "mask_build_s": round(cb["mask_build_s"], 3),
             "cpu_count": cb["cpu_count"], "cpu_model": cb["cpu_model"],
         }
