@@ -14,8 +14,11 @@
  * mtp_glora/data_utils/collator.py:123-124, 242-243, 308-309):
  *   - a [heads, seq, head_dim] operand is addressed as
  *       base + h * stride_h + s * stride_s + d     (elements; d contiguous)
- *   - dtype codes: MGA_DTYPE_BF16 or MGA_DTYPE_F32 (the model dtype);
- *     attention arithmetic is bf16 MFMA with fp32 accumulation in both cases.
+ *   - dtype codes: MGA_DTYPE_BF16, MGA_DTYPE_F16 or MGA_DTYPE_F32 (the
+ *     model dtype). Attention arithmetic: bf16 operands run bf16 MFMAs and
+ *     fp16 operands fp16 MFMAs, with fp32 accumulation and the probabilities
+ *     and dS rounded to the operand type before their products; fp32
+ *     operands are rounded to bf16 for the MFMAs.
  *   - the MTP mask is carried by one int32 code per chunk token:
  *       -1 pad, -2 regular token (x), >= 0 mask token (m) = its
  *       num_prefix_x value; every cached prefix key counts as x.
@@ -45,6 +48,7 @@ extern "C" {
 
 #define MGA_DTYPE_BF16 0
 #define MGA_DTYPE_F32 1
+#define MGA_DTYPE_F16 2
 
 #define MGA_BWD_DQ 1        /* mga_attn_bwd: delta = rowsum(o * dout), then dQ */
 #define MGA_BWD_DKDV 2      /* mga_attn_bwd: dK / dV (reads the delta of the dQ pass) */
@@ -283,7 +287,7 @@ int mga_gated_lora_bwd(const void *grad_y, int64_t gy_rs, const void *x, int64_t
  * Stable soft cross-entropy of the MTP sampler loss, row by row over n_rows
  * rows of n_cols logits (row r of a [rows, cols] operand starts at
  * base + r * row_stride elements; columns contiguous). For student logits x
- * and teacher logits t (the same dtype code, MGA_DTYPE_BF16 or MGA_DTYPE_F32):
+ * and teacher logits t (the same dtype code, MGA_DTYPE_BF16, MGA_DTYPE_F16 or MGA_DTYPE_F32):
  *   mx = max x, dx = max(sum e^{x - mx}, 1e-20), mt = max t,
  *   dt = max(sum e^{t - mt}, 1e-20),
  *   row_loss[r] = -(sum e^{t - mt} x) / dt + mx + log dx,

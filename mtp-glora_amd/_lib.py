@@ -21,6 +21,7 @@ MGA_ERR_CAPACITY = 2
 MGA_ERR_HIP = 3
 DTYPE_BF16 = 0
 DTYPE_F32 = 1
+DTYPE_F16 = 2
 BWD_DQ = 1
 BWD_DKDV = 2
 

@@ -41,15 +41,6 @@ constexpr int kThreads = 512;
 constexpr int kVRegular = 0x7ffffffe;
 constexpr int kVPadQuery = 0x7fffffff;
 
-typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2;
-
-__device__ __forceinline__ uint32_t cvt2(float x, float y) {
-  bf16x2 v;
-  v[0] = (bf16_t)x;
-  v[1] = (bf16_t)y;
-  return __builtin_bit_cast(uint32_t, v);
-}
-
 // Per-step bookkeeping of one group, carried from the load to the compute.
 struct StepInfo {
   int q0;       // first query row (chunk index)
@@ -120,6 +111,7 @@ struct GroupTile {
 
 template <int HD, typename T>
 __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_kernel(AttnArgs a, int kh0, int nkh) {
+  typedef typename MfmaElem<T>::type E;
   constexpr int KS = HD / 16;
   constexpr int DB = HD / 32;
   constexpr int TILE = kRows * HD;          // one group's tile (elements)
@@ -331,7 +323,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_kernel(AttnArgs a, 
       for (int ks = 0; ks < KS; ++ks) {
         bf16x8 nx;
         if (ks + 1 < KS) nx = lds_read8(reinterpret_cast<const bf16_t *>(lds_at(tQ, qk[ks + 1])));
-        sc = mfma32(op, kv[ks], sc);
+        sc = mfma32<E>(op, kv[ks], sc);
         if (ks + 1 < KS) op = nx;
       }
 #pragma unroll
@@ -355,14 +347,14 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_kernel(AttnArgs a, 
 #pragma unroll
       for (int u = 0; u < 2; ++u)
 #pragma unroll
-        for (int t = 0; t < 4; ++t) pw[u][t] = (int)cvt2(sc[8 * u + 2 * t], sc[8 * u + 2 * t + 1]) & keep;
+        for (int t = 0; t < 4; ++t) pw[u][t] = (int)cvt2<E>(sc[8 * u + 2 * t], sc[8 * u + 2 * t + 1]) & keep;
       char *pp = reinterpret_cast<char *>(pbuf(J % 2));
       *reinterpret_cast<i32x4 *>(pp + pofs) = pw[0];
       *reinterpret_cast<i32x4 *>(pp + pofs + 1024) = pw[1];
       // dV^T += dO^T P (16-row slice u, 32-dim block db)
 #pragma unroll
       for (int t = 0; t < 2 * DB; ++t)
-        acc[t % DB] = mfma32(tro.operand(tD, (t / DB) * 16, t % DB), __builtin_bit_cast(bf16x8, pw[t / DB]),
+        acc[t % DB] = mfma32<E>(tro.operand(tD, (t / DB) * 16, t % DB), __builtin_bit_cast(bf16x8, pw[t / DB]),
                              acc[t % DB]);
     } else {
       f32x16 &dp = dp2[J % 2];
@@ -380,14 +372,14 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_kernel(AttnArgs a, 
         for (int t = 0; t < 4; ++t) {
           // bit_cast of the element through a named scalar: bit_cast of a vector
           // subscript reads the vector's first element instead
-          const int wd = pws[u][t];
-          const bf16x2 pr = __builtin_bit_cast(bf16x2, wd);
-          dsw[u][t] = (int)cvt2((float)pr[0] * dprev[8 * u + 2 * t], (float)pr[1] * dprev[8 * u + 2 * t + 1]) & keep;
+          const uint32_t wd = (uint32_t)pws[u][t];
+          dsw[u][t] = (int)cvt2<E>(pair_lo<E>(wd) * dprev[8 * u + 2 * t], pair_hi<E>(wd) * dprev[8 * u + 2 * t + 1]) &
+                      keep;
         }
       }
 #pragma unroll
       for (int t = 0; t < 2 * DB; ++t)
-        acc[t % DB] = mfma32(tro.operand(tQprev, (t / DB) * 16, t % DB), __builtin_bit_cast(bf16x8, dsw[t / DB]),
+        acc[t % DB] = mfma32<E>(tro.operand(tQprev, (t / DB) * 16, t % DB), __builtin_bit_cast(bf16x8, dsw[t / DB]),
                              acc[t % DB]);
       // dP - delta = dO V^T + (-delta)
       dp = rows16(eb(J % 2), rofs);
@@ -396,7 +388,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_kernel(AttnArgs a, 
       for (int ks = 0; ks < KS; ++ks) {
         bf16x8 nx;
         if (ks + 1 < KS) nx = lds_read8(reinterpret_cast<const bf16_t *>(lds_at(tD, qk[ks + 1])));
-        dp = mfma32(op, kv[ks], dp);
+        dp = mfma32<E>(op, kv[ks], dp);
         if (ks + 1 < KS) op = nx;
       }
     }
@@ -481,14 +473,22 @@ void dkdv_launch(const AttnArgs &a, hipStream_t st) {
 template <int HD, typename T>
 void dq_launch(const AttnArgs &a, hipStream_t st);   // mga_bwd_dq.hip
 
-void launch_attn_bwd(const AttnArgs &a, int head_dim, bool is_f32, int passes, hipStream_t st) {
-  if (head_dim == 128) {
-    if (passes & kBwdDq) { if (is_f32) dq_launch<128, float>(a, st); else dq_launch<128, bf16_t>(a, st); }
-    if (passes & kBwdDkDv) { if (is_f32) dkdv_launch<128, float>(a, st); else dkdv_launch<128, bf16_t>(a, st); }
-  } else {
-    if (passes & kBwdDq) { if (is_f32) dq_launch<64, float>(a, st); else dq_launch<64, bf16_t>(a, st); }
-    if (passes & kBwdDkDv) { if (is_f32) dkdv_launch<64, float>(a, st); else dkdv_launch<64, bf16_t>(a, st); }
-  }
+template <int HD, typename T>
+static void bwd_launch(const AttnArgs &a, int passes, hipStream_t st) {
+  if (passes & kBwdDq) dq_launch<HD, T>(a, st);
+  if (passes & kBwdDkDv) dkdv_launch<HD, T>(a, st);
+}
+
+template <int HD>
+static void bwd_launch_dt(const AttnArgs &a, int dtype, int passes, hipStream_t st) {
+  if (dtype == kDtF32) bwd_launch<HD, float>(a, passes, st);
+  else if (dtype == kDtF16) bwd_launch<HD, f16_t>(a, passes, st);
+  else bwd_launch<HD, bf16_t>(a, passes, st);
+}
+
+void launch_attn_bwd(const AttnArgs &a, int head_dim, int dtype, int passes, hipStream_t st) {
+  if (head_dim == 128) bwd_launch_dt<128>(a, dtype, passes, st);
+  else bwd_launch_dt<64>(a, dtype, passes, st);
 }
 
 }  // namespace mga

@@ -34,7 +34,8 @@ __device__ __forceinline__ float half_row_dot(const T *o, const T *d, int hi) {
   for (int ks = 0; ks < HD / 16; ++ks) {
     const int c = ks * 16 + hi * 8;
     if constexpr (sizeof(T) == 2) {
-      const bf16x8 x = load8(o + c), y = load8(d + c);
+      const auto x = __builtin_bit_cast(typename Elem<T>::v8, load8(o + c));
+      const auto y = __builtin_bit_cast(typename Elem<T>::v8, load8(d + c));
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc += (float)x[e] * (float)y[e];
     } else {
@@ -51,6 +52,7 @@ __device__ __forceinline__ float half_row_dot(const T *o, const T *d, int hi) {
 
 template <int HD, typename T>
 __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnArgs a) {
+  typedef typename MfmaElem<T>::type E;
   constexpr int KS = HD / 16;
   constexpr int DB = HD / 32;
   constexpr int TILE = kStep * HD;
@@ -180,8 +182,8 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnArgs a) {
           vn = rd(tV, ks + 1);
         }
         __builtin_amdgcn_sched_barrier(0);
-        sacc = mfma32(kc, qf[ks], sacc);
-        dpacc = mfma32(vc, dof[ks], dpacc);
+        sacc = mfma32<E>(kc, qf[ks], sacc);
+        dpacc = mfma32<E>(vc, dof[ks], dpacc);
         __builtin_amdgcn_sched_barrier(0);
         if (ks + 1 < KS) {
           kc = kn;
@@ -207,11 +209,11 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnArgs a) {
       // dQ^T += K^T dS^T
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
-        const bf16x8 dsb = pack8(dpacc[8 * u + 0], dpacc[8 * u + 1], dpacc[8 * u + 2], dpacc[8 * u + 3],
+        const bf16x8 dsb = pack8<E>(dpacc[8 * u + 0], dpacc[8 * u + 1], dpacc[8 * u + 2], dpacc[8 * u + 3],
                                  dpacc[8 * u + 4], dpacc[8 * u + 5], dpacc[8 * u + 6], dpacc[8 * u + 7]);
 #pragma unroll
         for (int db = 0; db < DB; ++db)
-          dqacc[db] = mfma32(tro.operand(tK, 16 * u, db), dsb, dqacc[db]);
+          dqacc[db] = mfma32<E>(tro.operand(tK, 16 * u, db), dsb, dqacc[db]);
       }
     }
 
@@ -255,5 +257,7 @@ template void dq_launch<128, bf16_t>(const AttnArgs &, hipStream_t);
 template void dq_launch<128, float>(const AttnArgs &, hipStream_t);
 template void dq_launch<64, bf16_t>(const AttnArgs &, hipStream_t);
 template void dq_launch<64, float>(const AttnArgs &, hipStream_t);
+template void dq_launch<128, f16_t>(const AttnArgs &, hipStream_t);
+template void dq_launch<64, f16_t>(const AttnArgs &, hipStream_t);
 
 }  // namespace mga

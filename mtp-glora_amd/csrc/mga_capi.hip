@@ -11,6 +11,8 @@
 #include "mga_internal.hpp"
 
 static_assert(MGA_BWD_DQ == mga::kBwdDq && MGA_BWD_DKDV == mga::kBwdDkDv, "pass flags");
+static_assert(MGA_DTYPE_BF16 == mga::kDtBf16 && MGA_DTYPE_F32 == mga::kDtF32 && MGA_DTYPE_F16 == mga::kDtF16,
+              "dtype codes");
 
 namespace {
 
@@ -33,7 +35,9 @@ int check_launch(const char *what) {
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
-int elem_bytes(int dtype) { return dtype == MGA_DTYPE_BF16 ? 2 : (dtype == MGA_DTYPE_F32 ? 4 : 0); }
+int elem_bytes(int dtype) {
+  return (dtype == MGA_DTYPE_BF16 || dtype == MGA_DTYPE_F16) ? 2 : (dtype == MGA_DTYPE_F32 ? 4 : 0);
+}
 
 // A [heads, rows, head_dim] operand addressed with element strides: every row
 // start must be 16-byte aligned for the vector loads.
@@ -183,7 +187,7 @@ int mga_attn_fwd(const void *q, int64_t q_sh, int64_t q_ss, const void *k, int64
   a.nKV = (L + MGA_BLOCK - 1) / MGA_BLOCK;
   a.scale = scale;
   a.scale_log2 = scale * mga::kLog2e;
-  mga::launch_attn_fwd(a, head_dim, dtype == MGA_DTYPE_F32, (hipStream_t)stream);
+  mga::launch_attn_fwd(a, head_dim, dtype, (hipStream_t)stream);
   return check_launch("mga_attn_fwd");
 }
 
@@ -236,7 +240,7 @@ int mga_attn_bwd(const void *q, int64_t q_sh, int64_t q_ss, const void *k, int64
   a.nKV = (L + MGA_BLOCK - 1) / MGA_BLOCK;
   a.scale = scale;
   a.scale_log2 = scale * mga::kLog2e;
-  mga::launch_attn_bwd(a, head_dim, dtype == MGA_DTYPE_F32, passes, (hipStream_t)stream);
+  mga::launch_attn_bwd(a, head_dim, dtype, passes, (hipStream_t)stream);
   return check_launch("mga_attn_bwd");
 }
 
@@ -294,7 +298,7 @@ int mga_qk_norm_rope_fwd(const void *q, int64_t q_ss, int64_t q_hs, const void *
   a.qo = q_out; a.qo_ss = qo_ss; a.qo_hs = qo_hs;
   a.ko = k_out; a.ko_ss = ko_ss; a.ko_hs = ko_hs;
   a.rstd = rstd; a.eps = eps; a.S = S; a.Hq = Hq; a.Hkv = Hkv; a.D = head_dim;
-  mga::launch_qk_norm_rope(a, dtype == MGA_DTYPE_F32, false, (hipStream_t)stream);
+  mga::launch_qk_norm_rope(a, dtype, false, (hipStream_t)stream);
   return check_launch("mga_qk_norm_rope_fwd");
 }
 
@@ -316,7 +320,7 @@ int mga_qk_norm_rope_bwd(const void *q, int64_t q_ss, int64_t q_hs, const void *
   a.dq = dq; a.dq_ss = dq_ss; a.dq_hs = dq_hs;
   a.dk = dk; a.dk_ss = dk_ss; a.dk_hs = dk_hs;
   a.rstd = const_cast<float *>(rstd); a.S = S; a.Hq = Hq; a.Hkv = Hkv; a.D = head_dim;
-  mga::launch_qk_norm_rope(a, dtype == MGA_DTYPE_F32, true, (hipStream_t)stream);
+  mga::launch_qk_norm_rope(a, dtype, true, (hipStream_t)stream);
   return check_launch("mga_qk_norm_rope_bwd");
 }
 
@@ -546,7 +550,7 @@ int mga_soft_ce_fwd(const void *student, int64_t student_row_stride, const void 
   if (rc != MGA_OK) return rc;
   if (!row_loss || !stats || !workspace) return fail(MGA_ERR_INVALID, "mga_soft_ce_fwd: null output or workspace");
   mga::launch_soft_ce_fwd(student, student_row_stride, teacher, teacher_row_stride, n_rows, n_cols,
-                          dtype == MGA_DTYPE_F32, vec, row_loss, stats, workspace, (hipStream_t)stream);
+                          dtype, vec, row_loss, stats, workspace, (hipStream_t)stream);
   return check_launch("mga_soft_ce_fwd");
 }
 
@@ -560,7 +564,7 @@ int mga_soft_ce_bwd(const void *student, int64_t student_row_stride, const void 
   if (rc != MGA_OK) return rc;
   if (!grad_output || !stats) return fail(MGA_ERR_INVALID, "mga_soft_ce_bwd: null grad_output or stats");
   mga::launch_soft_ce_bwd(student, student_row_stride, teacher, teacher_row_stride, n_rows, n_cols,
-                          dtype == MGA_DTYPE_F32, vec, grad_output, stats, grad, grad_row_stride, (hipStream_t)stream);
+                          dtype, vec, grad_output, stats, grad, grad_row_stride, (hipStream_t)stream);
   return check_launch("mga_soft_ce_bwd");
 }
 

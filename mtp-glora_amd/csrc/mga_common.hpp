@@ -5,8 +5,15 @@
 #include <stdint.h>
 
 typedef __bf16 bf16_t;
+typedef _Float16 f16_t;
+// bf16x8 is also the carrier of any 16-byte MFMA operand fragment: fp16
+// fragments travel in it as raw bits and are reinterpreted at the MFMA.
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
 typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4;
+typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2;
+typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 f16x8;
+typedef __attribute__((__vector_size__(4 * sizeof(_Float16)))) _Float16 f16x4;
+typedef __attribute__((__vector_size__(2 * sizeof(_Float16)))) _Float16 f16x2;
 typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
 typedef __attribute__((__vector_size__(4 * sizeof(int)))) int i32x4;
@@ -26,6 +33,11 @@ __device__ __forceinline__ bf16x8 load8(const bf16_t *p) {
   return __builtin_bit_cast(bf16x8, *reinterpret_cast<const i32x4 *>(p));
 }
 
+// fp16 elements: the raw bits (an fp16 MFMA fragment)
+__device__ __forceinline__ bf16x8 load8(const f16_t *p) {
+  return __builtin_bit_cast(bf16x8, *reinterpret_cast<const i32x4 *>(p));
+}
+
 __device__ __forceinline__ bf16x8 load8(const float *p) {
   const f32x4 a = *reinterpret_cast<const f32x4 *>(p);
   const f32x4 b = *reinterpret_cast<const f32x4 *>(p + 4);
@@ -40,6 +52,12 @@ __device__ __forceinline__ bf16x8 load8(const float *p) {
 __device__ __forceinline__ void store4(bf16_t *p, float a, float b, float c, float d) {
   bf16x4 v;
   v[0] = (bf16_t)a; v[1] = (bf16_t)b; v[2] = (bf16_t)c; v[3] = (bf16_t)d;
+  *reinterpret_cast<i32x2 *>(p) = __builtin_bit_cast(i32x2, v);
+}
+
+__device__ __forceinline__ void store4(f16_t *p, float a, float b, float c, float d) {
+  f16x4 v;
+  v[0] = (f16_t)a; v[1] = (f16_t)b; v[2] = (f16_t)c; v[3] = (f16_t)d;
   *reinterpret_cast<i32x2 *>(p) = __builtin_bit_cast(i32x2, v);
 }
 
@@ -62,18 +80,68 @@ __device__ __forceinline__ bf16x8 lds_read4x2(const bf16_t *p0, const bf16_t *p1
   return __builtin_bit_cast(bf16x8, r);
 }
 
-// Eight fp32 accumulator values -> one bf16 MFMA operand.
+// ---- the 16-bit MFMA element E (bf16_t or f16_t) ---------------------------
+// Operand fragments are 8 elements of E carried as bf16x8 bits; conversions
+// from fp32 round to nearest even.
+
+template <typename E> struct Elem;
+template <> struct Elem<bf16_t> { typedef bf16x8 v8; typedef bf16x2 v2; };
+template <> struct Elem<f16_t> { typedef f16x8 v8; typedef f16x2 v2; };
+
+// Eight fp32 accumulator values -> one MFMA operand of E.
+template <typename E>
 __device__ __forceinline__ bf16x8 pack8(float a0, float a1, float a2, float a3,
                                         float a4, float a5, float a6, float a7) {
-  bf16x8 r;
-  r[0] = (bf16_t)a0; r[1] = (bf16_t)a1; r[2] = (bf16_t)a2; r[3] = (bf16_t)a3;
-  r[4] = (bf16_t)a4; r[5] = (bf16_t)a5; r[6] = (bf16_t)a6; r[7] = (bf16_t)a7;
-  return r;
+  typename Elem<E>::v8 r;
+  r[0] = (E)a0; r[1] = (E)a1; r[2] = (E)a2; r[3] = (E)a3;
+  r[4] = (E)a4; r[5] = (E)a5; r[6] = (E)a6; r[7] = (E)a7;
+  return __builtin_bit_cast(bf16x8, r);
 }
 
-__device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
+// Two fp32 values -> one packed pair of E (x in the low half).
+template <typename E>
+__device__ __forceinline__ uint32_t cvt2(float x, float y) {
+  typename Elem<E>::v2 v;
+  v[0] = (E)x;
+  v[1] = (E)y;
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// The two elements of a packed pair, as fp32.
+template <typename E>
+__device__ __forceinline__ float pair_lo(uint32_t w) { return (float)__builtin_bit_cast(typename Elem<E>::v2, w)[0]; }
+template <typename E>
+__device__ __forceinline__ float pair_hi(uint32_t w) { return (float)__builtin_bit_cast(typename Elem<E>::v2, w)[1]; }
+
+// acc + both elements of a packed pair (one v_dot2 against (1, 1)).
+template <typename E> __device__ __forceinline__ float add_pair(uint32_t p, float acc);
+template <>
+__device__ __forceinline__ float add_pair<bf16_t>(uint32_t p, float acc) {
+  const bf16x2 one = {(bf16_t)1.0f, (bf16_t)1.0f};
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, p), one, acc, false);
+}
+template <>
+__device__ __forceinline__ float add_pair<f16_t>(uint32_t p, float acc) {
+  const f16x2 one = {(f16_t)1.0f, (f16_t)1.0f};
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, p), one, acc, false);
+}
+
+// One 32x32x16 MFMA of E operands into fp32.
+template <typename E> __device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c);
+template <>
+__device__ __forceinline__ f32x16 mfma32<bf16_t>(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
+template <>
+__device__ __forceinline__ f32x16 mfma32<f16_t>(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
+                                                0, 0);
+}
+
+// The MFMA element of a storage type: fp16 data computes in fp16, bf16 data
+// in bf16 (fp32 data does not use these kernels).
+template <typename T> struct MfmaElem { typedef bf16_t type; };
+template <> struct MfmaElem<f16_t> { typedef f16_t type; };
 
 __device__ __forceinline__ f32x16 zero16() {
   f32x16 z;

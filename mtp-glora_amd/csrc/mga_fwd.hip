@@ -39,28 +39,15 @@ namespace mga {
 namespace {
 
 constexpr float kNegInfF = -__builtin_huge_valf();
-constexpr float kPBound = 1048576.f;   // 2^20: largest partial row sum of a step on the fast path
+// Largest partial row sum of a step on the fast path (so also the largest
+// probability): 2^20 for bf16, 2^15 for fp16 (whose largest finite is 65504).
+template <typename E>
+constexpr float kPBound = std::is_same_v<E, f16_t> ? 32768.f : 1048576.f;
 constexpr int kStepKeys = 64;                 // keys per pipeline step (a multiple of 32)
 constexpr int kStepBlocks = kStepKeys / 32;   // 32-key MFMA blocks per step
 constexpr int kStepsPerTile = kBlock / kStepKeys;
 
-typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2;
-
 __device__ __forceinline__ float exp2f_(float x) { return __builtin_amdgcn_exp2f(x); }
-
-// two probabilities -> one packed bf16 pair (round to nearest even)
-__device__ __forceinline__ uint32_t cvt2(float x, float y) {
-  bf16x2 v;
-  v[0] = (bf16_t)x;
-  v[1] = (bf16_t)y;
-  return __builtin_bit_cast(uint32_t, v);
-}
-
-// acc + the two bf16 values of p
-__device__ __forceinline__ float add_pair(uint32_t p, float acc) {
-  const bf16x2 one = {(bf16_t)1.0f, (bf16_t)1.0f};
-  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, p), one, acc, false);
-}
 
 // Heads sharing a workgroup (a divisor of both G and 4).
 __host__ __device__ __forceinline__ int heads_per_wg(int G) { return (G % 4 == 0) ? 4 : (G % 2 == 0 ? 2 : 1); }
@@ -69,6 +56,7 @@ __host__ __device__ __forceinline__ int heads_per_wg(int G) { return (G % 4 == 0
 
 template <int NB, int HD, typename T>
 __global__ __launch_bounds__(256, 3 - NB) void attn_fwd_kernel(AttnArgs a) {
+  typedef typename MfmaElem<T>::type E;
   constexpr int KS = HD / 16;          // k-steps of QK^T over head_dim
   constexpr int DB = HD / 32;          // 32-dim blocks of O^T
   constexpr int TILE = kStepKeys * HD; // elements of one K or V step tile
@@ -214,7 +202,7 @@ __global__ __launch_bounds__(256, 3 - NB) void attn_fwd_kernel(AttnArgs a) {
 #pragma unroll
         for (int kb = 0; kb < kStepBlocks; ++kb)
 #pragma unroll
-          for (int nb = 0; nb < NB; ++nb) sacc[kb][nb] = mfma32(ka[kb], qf[nb][ks], sacc[kb][nb]);
+          for (int nb = 0; nb < NB; ++nb) sacc[kb][nb] = mfma32<E>(ka[kb], qf[nb][ks], sacc[kb][nb]);
         __builtin_amdgcn_sched_barrier(0);
         if (ks + 1 < KS)
 #pragma unroll
@@ -252,16 +240,16 @@ __global__ __launch_bounds__(256, 3 - NB) void attn_fwd_kernel(AttnArgs a) {
               for (int t = 0; t < 4; ++t) {
                 const float p0 = exp2f_(__builtin_fmaf(sacc[kb][nb][8 * u + 2 * t], c, -m));
                 const float p1 = exp2f_(__builtin_fmaf(sacc[kb][nb][8 * u + 2 * t + 1], c, -m));
-                const uint32_t w = cvt2(p0, p1);
+                const uint32_t w = cvt2<E>(p0, p1);
                 wv[t] = (int)w;
-                ps = add_pair(w, ps);
+                ps = add_pair<E>(w, ps);
               }
               pb[nb][2 * kb + u] = __builtin_bit_cast(bf16x8, wv);
             }
           return ps;
         };
         float ps = probs(m_run[nb]);
-        if (__builtin_amdgcn_ballot_w64(!(ps <= kPBound))) {
+        if (__builtin_amdgcn_ballot_w64(!(ps <= kPBound<E>))) {
           float mx = kNegInfF;
 #pragma unroll
           for (int kb = 0; kb < kStepBlocks; ++kb)
@@ -291,7 +279,7 @@ __global__ __launch_bounds__(256, 3 - NB) void attn_fwd_kernel(AttnArgs a) {
         if (t + 1 < 2 * kStepBlocks * DB) vnext = tro.operand(tV, ((t + 1) / DB) * 16, (t + 1) % DB);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb) oacc[nb][t % DB] = mfma32(vcur, pb[nb][t / DB], oacc[nb][t % DB]);
+        for (int nb = 0; nb < NB; ++nb) oacc[nb][t % DB] = mfma32<E>(vcur, pb[nb][t / DB], oacc[nb][t % DB]);
         __builtin_amdgcn_sched_barrier(0);
         if (t + 1 < 2 * kStepBlocks * DB) vcur = vnext;
       }
@@ -337,6 +325,8 @@ __global__ __launch_bounds__(256, 3 - NB) void attn_fwd_kernel(AttnArgs a) {
 // this template (the bf16 ones), leaving undefined symbols
 template __global__ void attn_fwd_kernel<1, 128, bf16_t>(AttnArgs);
 template __global__ void attn_fwd_kernel<1, 64, bf16_t>(AttnArgs);
+template __global__ void attn_fwd_kernel<1, 128, f16_t>(AttnArgs);
+template __global__ void attn_fwd_kernel<1, 64, f16_t>(AttnArgs);
 template __global__ void attn_fwd_kernel<1, 128, float>(AttnArgs);
 template __global__ void attn_fwd_kernel<1, 64, float>(AttnArgs);
 
@@ -353,12 +343,16 @@ static void fwd_launch(const AttnArgs &a, hipStream_t st) {
   hipLaunchKernelGGL((attn_fwd_kernel<NB, HD, T>), dim3(items), dim3(256), 0, st, a);
 }
 
-void launch_attn_fwd(const AttnArgs &a, int head_dim, bool is_f32, hipStream_t st) {
-  if (head_dim == 128) {
-    if (is_f32) fwd_launch<128, float>(a, st); else fwd_launch<128, bf16_t>(a, st);
-  } else {
-    if (is_f32) fwd_launch<64, float>(a, st); else fwd_launch<64, bf16_t>(a, st);
-  }
+template <int HD>
+static void fwd_launch_dt(const AttnArgs &a, int dtype, hipStream_t st) {
+  if (dtype == kDtF32) fwd_launch<HD, float>(a, st);
+  else if (dtype == kDtF16) fwd_launch<HD, f16_t>(a, st);
+  else fwd_launch<HD, bf16_t>(a, st);
+}
+
+void launch_attn_fwd(const AttnArgs &a, int head_dim, int dtype, hipStream_t st) {
+  if (head_dim == 128) fwd_launch_dt<128>(a, dtype, st);
+  else fwd_launch_dt<64>(a, dtype, st);
 }
 
 }  // namespace mga

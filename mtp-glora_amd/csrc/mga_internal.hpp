@@ -39,12 +39,17 @@ void launch_mtp_block_mask(const int64_t *gate, int64_t gate_stride, int32_t S, 
                            int32_t *q_idx, int32_t *full_q_num, int32_t *full_q_idx,
                            hipStream_t stream);
 
-// head_dim in {64, 128}; is_f32 selects fp32 operands (else bf16).
-void launch_attn_fwd(const AttnArgs &a, int head_dim, bool is_f32, hipStream_t stream);
+// Element types of the operands (the C ABI's MGA_DTYPE_* codes).
+constexpr int kDtBf16 = 0;
+constexpr int kDtF32 = 1;
+constexpr int kDtF16 = 2;
+
+// head_dim in {64, 128}; dtype one of kDt*.
+void launch_attn_fwd(const AttnArgs &a, int head_dim, int dtype, hipStream_t stream);
 // passes: kBwdDq (delta + dQ) and/or kBwdDkDv (dK/dV; reads the delta the dQ pass wrote).
 constexpr int kBwdDq = 1;
 constexpr int kBwdDkDv = 2;
-void launch_attn_bwd(const AttnArgs &a, int head_dim, bool is_f32, int passes, hipStream_t stream);
+void launch_attn_bwd(const AttnArgs &a, int head_dim, int dtype, int passes, hipStream_t stream);
 
 // Fused Qwen3 q/k RMSNorm + rotary embedding (mga_qk_rope.hip). Operands are
 // [S, heads, D] addressed with (token stride, head stride) in elements; cos
@@ -63,7 +68,7 @@ struct QkRopeArgs {
   float eps;
   int32_t S, Hq, Hkv, D;
 };
-void launch_qk_norm_rope(const QkRopeArgs &a, bool is_f32, bool backward, hipStream_t stream);
+void launch_qk_norm_rope(const QkRopeArgs &a, int dtype, bool backward, hipStream_t stream);
 
 // Plain bf16 GEMM through hipBLASLt, row-major (mga_blas.hip):
 // D[M, N] = op(A)[M, K] op(B)[K, N] (+ D), op(A) = A^T when ta (A stored
@@ -117,9 +122,9 @@ void launch_lora_transpose(const void *A, int64_t a_rs, int32_t rank, int32_t K,
 // Stable soft cross-entropy (mga_soft_ce.hip). Rows of V columns; row strides
 // in elements; vec: 16-byte vector loads (every row start 16-byte aligned).
 int64_t soft_ce_workspace_floats(int32_t n_rows, int32_t n_cols);
-void launch_soft_ce_fwd(const void *x, int64_t xs, const void *t, int64_t ts, int32_t N, int32_t V, bool is_f32,
+void launch_soft_ce_fwd(const void *x, int64_t xs, const void *t, int64_t ts, int32_t N, int32_t V, int dtype,
                         bool vec, float *loss, float *stats, float *ws, hipStream_t stream);
-void launch_soft_ce_bwd(const void *x, int64_t xs, const void *t, int64_t ts, int32_t N, int32_t V, bool is_f32,
+void launch_soft_ce_bwd(const void *x, int64_t xs, const void *t, int64_t ts, int32_t N, int32_t V, int dtype,
                         bool vec, const float *grad_out, const float *stats, void *g, int64_t gs,
                         hipStream_t stream);
 

@@ -132,7 +132,7 @@ __global__ __launch_bounds__(kDownWaves * 64) void lora_down_kernel(LoraDownArgs
       if (row_ok && hr) *reinterpret_cast<i32x4 *>(hr + k0) = __builtin_bit_cast(i32x4, xv);
     }
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) acc[nb] = mfma32(xv, av[nb], acc[nb]);
+    for (int nb = 0; nb < NB; ++nb) acc[nb] = mfma32<bf16_t>(xv, av[nb], acc[nb]);
   };
   auto load_step = [&](bf16x8 &xv, bf16x8 (&av)[NB], int step) {
     const int k0 = 16 * (w + kDownWaves * step);
@@ -315,7 +315,7 @@ __global__ __launch_bounds__(256) void lora_down_ring_kernel(LoraDownArgs a) {
           if (row_ok) *reinterpret_cast<i32x4 *>(hr + k0) = __builtin_bit_cast(i32x4, xv);
       }
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb) acc[nb] = mfma32(xv, opc[j][nb], acc[nb]);
+      for (int nb = 0; nb < NB; ++nb) acc[nb] = mfma32<bf16_t>(xv, opc[j][nb], acc[nb]);
     }
     load_ops(c + 1, opn);
   };
@@ -443,7 +443,7 @@ __global__ __launch_bounds__(256) void lora_dx_kernel(LoraDxArgs a) {
     f32x16 acc = zero16();
     const bf16_t *brow = sAt + (blk * 32 + l32) * LS + 8 * hi;
 #pragma unroll
-    for (int j = 0; j < NK; ++j) acc = mfma32(dv[j], lds_read8(brow + 16 * j), acc);
+    for (int j = 0; j < NK; ++j) acc = mfma32<bf16_t>(dv[j], lds_read8(brow + 16 * j), acc);
     // d(dropout(x)) = T(d_a A): lane holds column l32 of rows 8 (q / 4) + 4 hi + q % 4
 #pragma unroll
     for (int q = 0; q < 16; ++q) tile[(8 * (q >> 2) + 4 * hi + (q & 3)) * TS + l32] = (bf16_t)acc[q];
@@ -511,7 +511,7 @@ __global__ __launch_bounds__(256) void lora_dx_rows_kernel(LoraDxArgs a) {
 #pragma unroll
     for (int blk = 0; blk < 4; ++blk)
 #pragma unroll
-      for (int j = 0; j < NK; ++j) acc[blk] = mfma32(av[blk][j], dv[j], acc[blk]);
+      for (int j = 0; j < NK; ++j) acc[blk] = mfma32<bf16_t>(av[blk][j], dv[j], acc[blk]);
   }
 #pragma unroll
   for (int blk = 0; blk < 4; ++blk) {
@@ -615,7 +615,7 @@ __global__ __launch_bounds__(256) void lora_da_kernel(LoraDaArgs a, int r0) {
     for (int ss = 0; ss < 2; ++ss) {
       const bf16x8 hb = tro.operand(tx, 16 * ss, w);
 #pragma unroll
-      for (int rb = 0; rb < NB; ++rb) acc[rb] = mfma32(tro.operand(td, 16 * ss, rb), hb, acc[rb]);
+      for (int rb = 0; rb < NB; ++rb) acc[rb] = mfma32<bf16_t>(tro.operand(td, 16 * ss, rb), hb, acc[rb]);
     }
     if (st + 1 < st1) store(B ? sX0 : sX1, B ? sD0 : sD1);
     __syncthreads();

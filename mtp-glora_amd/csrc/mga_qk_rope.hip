@@ -60,6 +60,19 @@ template <>
 struct Rnd<bf16_t> {
   __device__ __forceinline__ static float one(float v) { return __uint_as_float(pk_bf16(0.f, v)); }
 };
+// fp16: round to nearest even and back, as two instructions the optimiser
+// cannot fold (folded into packed fp16 arithmetic, this kernel's fp16 form
+// fails instruction selection with packed fp32 disabled)
+template <>
+struct Rnd<f16_t> {
+  __device__ __forceinline__ static float one(float v) {
+    uint32_t h;
+    float r;
+    asm("v_cvt_f16_f32 %0, %1" : "=v"(h) : "v"(v));
+    asm("v_cvt_f32_f16 %0, %1" : "=v"(r) : "v"(h));
+    return r;
+  }
+};
 
 // V consecutive elements of T <-> fp32.
 template <typename T, int V>
@@ -73,35 +86,29 @@ struct Elems {
     for (int i = 0; i < V; ++i) p[i] = (T)v[i];
   }
 };
-template <>
-struct Elems<bf16_t, 8> {
-  __device__ __forceinline__ static void load(const bf16_t *p, float (&v)[8]) {
-    const bf16x8 a = load8(p);
+// 16-bit elements (bf16, fp16), V = 8 (16 bytes) or 4 (8 bytes)
+template <typename T, int V>
+struct Elems16 {
+  typedef T vt __attribute__((ext_vector_type(V)));
+  __device__ __forceinline__ static void load(const T *p, float (&v)[V]) {
+    const vt a = *reinterpret_cast<const vt *>(p);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = (float)a[i];
+    for (int i = 0; i < V; ++i) v[i] = (float)a[i];
   }
-  // non-temporal: the outputs are streamed once and read by a later kernel
-  __device__ __forceinline__ static void store(bf16_t *p, const float (&v)[8]) {
-    bf16x8 a;
+  __device__ __forceinline__ static void store(T *p, const float (&v)[V]) {
+    vt a;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) a[i] = (bf16_t)v[i];
-    __builtin_nontemporal_store(__builtin_bit_cast(i32x4, a), reinterpret_cast<i32x4 *>(p));
-  }
-};
-template <>
-struct Elems<bf16_t, 4> {
-  __device__ __forceinline__ static void load(const bf16_t *p, float (&v)[4]) {
-    const bf16x4 a = *reinterpret_cast<const bf16x4 *>(p);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = (float)a[i];
-  }
-  __device__ __forceinline__ static void store(bf16_t *p, const float (&v)[4]) {
-    bf16x4 a;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) a[i] = (bf16_t)v[i];
-    *reinterpret_cast<bf16x4 *>(p) = a;
+    for (int i = 0; i < V; ++i) a[i] = (T)v[i];
+    if constexpr (V == 8)   // non-temporal: the outputs are streamed once and read by a later kernel
+      __builtin_nontemporal_store(__builtin_bit_cast(i32x4, a), reinterpret_cast<i32x4 *>(p));
+    else
+      *reinterpret_cast<vt *>(p) = a;
   }
 };
+template <> struct Elems<bf16_t, 8> : Elems16<bf16_t, 8> {};
+template <> struct Elems<bf16_t, 4> : Elems16<bf16_t, 4> {};
+template <> struct Elems<f16_t, 8> : Elems16<f16_t, 8> {};
+template <> struct Elems<f16_t, 4> : Elems16<f16_t, 4> {};
 template <>
 struct Elems<float, 4> {
   __device__ __forceinline__ static void load(const float *p, float (&v)[4]) {
@@ -285,7 +292,7 @@ void launch_v(const QkRopeArgs &a, bool backward, hipStream_t st) {
 
 template <typename T>
 void launch_typed(const QkRopeArgs &a, bool backward, hipStream_t st) {
-  constexpr int kWide = 16 / (int)sizeof(T);   // 8 bf16 or 4 fp32 per 16-byte access
+  constexpr int kWide = 16 / (int)sizeof(T);   // 8 bf16 / fp16 or 4 fp32 per 16-byte access
   if (vec_ok(a, backward, kWide, (int)sizeof(T))) launch_v<T, kWide>(a, backward, st);
   else if (sizeof(T) == 2 && vec_ok(a, backward, 4, 2)) launch_v<T, 4>(a, backward, st);
   else launch_v<T, 1>(a, backward, st);
@@ -293,8 +300,9 @@ void launch_typed(const QkRopeArgs &a, bool backward, hipStream_t st) {
 
 }  // namespace
 
-void launch_qk_norm_rope(const QkRopeArgs &a, bool is_f32, bool backward, hipStream_t st) {
-  if (is_f32) launch_typed<float>(a, backward, st);
+void launch_qk_norm_rope(const QkRopeArgs &a, int dtype, bool backward, hipStream_t st) {
+  if (dtype == kDtF32) launch_typed<float>(a, backward, st);
+  else if (dtype == kDtF16) launch_typed<f16_t>(a, backward, st);
   else launch_typed<bf16_t>(a, backward, st);
 }
 

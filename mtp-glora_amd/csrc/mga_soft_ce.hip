@@ -89,20 +89,19 @@ struct Stats {
   }
 };
 
+// 16-byte vectors of the element type <-> fp32.
 template <typename T>
-struct Vec;
-template <>
-struct Vec<bf16_t> {
+struct Vec {   // bf16 and fp16
   static constexpr int W = 8;
-  __device__ __forceinline__ static void load(const bf16_t *p, float (&v)[W]) {
-    const bf16x8 a = load8(p);
+  __device__ __forceinline__ static void load(const T *p, float (&v)[W]) {
+    const auto a = __builtin_bit_cast(typename Elem<T>::v8, load8(p));
 #pragma unroll
     for (int i = 0; i < W; ++i) v[i] = (float)a[i];
   }
-  __device__ __forceinline__ static void store(bf16_t *p, const float (&v)[W]) {
-    bf16x8 a;
+  __device__ __forceinline__ static void store(T *p, const float (&v)[W]) {
+    typename Elem<T>::v8 a;
 #pragma unroll
-    for (int i = 0; i < W; ++i) a[i] = (bf16_t)v[i];
+    for (int i = 0; i < W; ++i) a[i] = (T)v[i];
     *reinterpret_cast<i32x4 *>(p) = __builtin_bit_cast(i32x4, a);
   }
 };
@@ -295,15 +294,17 @@ static void bwd_typed(const void *x, int64_t xs, const void *t, int64_t ts, int3
                        (const T *)t, ts, V, ch, ns, N, go, stats, (T *)g, gs);
 }
 
-void launch_soft_ce_fwd(const void *x, int64_t xs, const void *t, int64_t ts, int32_t N, int32_t V, bool is_f32,
+void launch_soft_ce_fwd(const void *x, int64_t xs, const void *t, int64_t ts, int32_t N, int32_t V, int dtype,
                         bool vec, float *loss, float *stats, float *ws, hipStream_t st) {
-  if (is_f32) fwd_typed<float>(x, xs, t, ts, N, V, vec, loss, stats, ws, st);
+  if (dtype == kDtF32) fwd_typed<float>(x, xs, t, ts, N, V, vec, loss, stats, ws, st);
+  else if (dtype == kDtF16) fwd_typed<f16_t>(x, xs, t, ts, N, V, vec, loss, stats, ws, st);
   else fwd_typed<bf16_t>(x, xs, t, ts, N, V, vec, loss, stats, ws, st);
 }
 
-void launch_soft_ce_bwd(const void *x, int64_t xs, const void *t, int64_t ts, int32_t N, int32_t V, bool is_f32,
+void launch_soft_ce_bwd(const void *x, int64_t xs, const void *t, int64_t ts, int32_t N, int32_t V, int dtype,
                         bool vec, const float *go, const float *stats, void *g, int64_t gs, hipStream_t st) {
-  if (is_f32) bwd_typed<float>(x, xs, t, ts, N, V, vec, go, stats, g, gs, st);
+  if (dtype == kDtF32) bwd_typed<float>(x, xs, t, ts, N, V, vec, go, stats, g, gs, st);
+  else if (dtype == kDtF16) bwd_typed<f16_t>(x, xs, t, ts, N, V, vec, go, stats, g, gs, st);
   else bwd_typed<bf16_t>(x, xs, t, ts, N, V, vec, go, stats, g, gs, st);
 }
 

@@ -30,9 +30,11 @@ def _dev(name: str, t: torch.Tensor) -> None:
 def dtype_code(dt: torch.dtype) -> int:
     if dt == torch.bfloat16:
         return _lib.DTYPE_BF16
+    if dt == torch.float16:
+        return _lib.DTYPE_F16
     if dt == torch.float32:
         return _lib.DTYPE_F32
-    raise TypeError(f"unsupported dtype {dt}; expected bfloat16 or float32")
+    raise TypeError(f"unsupported dtype {dt}; expected bfloat16, float16 or float32")
 
 
 def _rows(name: str, t: torch.Tensor):

@@ -14,8 +14,8 @@ checkout), per row x of D elements (one head of one token) in the model dtype T:
       n   = T(w * T(x * r)),
       out = T(T(n * cos) + T(rotate_half(n) * sin)),
       rotate_half(n) = [-n[D/2:], n[:D/2]],
-  where T rounds fp32 to bf16 (round to nearest even) for bf16 operands and is
-  the identity for fp32 ones. Each torch op on bf16 tensors computes in fp32
+  where T rounds fp32 to the model dtype (round to nearest even) for bf16 and
+  fp16 operands and is the identity for fp32 ones. Each torch op on bf16 tensors computes in fp32
   and rounds once, which is what T after every op restates. The mean is
   numpy's fp32 sum times fp32(1/D) (torch's mean reduction multiplies by the
   reciprocal of the count), and r is the correctly rounded fp32 of the
@@ -41,15 +41,28 @@ def bf16_round(a) -> np.ndarray:
     return u.astype(np.uint32).view(np.float32)
 
 
-def _rounder(bf16: bool):
-    return bf16_round if bf16 else (lambda a: np.asarray(a, dtype=np.float32))
+def f16_round(a) -> np.ndarray:
+    """fp32 -> nearest fp16 (ties to even; past 65504 -> inf), returned as fp32."""
+    with np.errstate(over="ignore"):
+        return np.asarray(a, dtype=np.float32).astype(np.float16).astype(np.float32)
 
 
-def norm_rope(x, w, cos, sin, eps: float, bf16: bool):
+def _rounder(rnd):
+    if rnd is True or rnd == "bf16":
+        return bf16_round
+    if rnd == "f16":
+        return f16_round
+    if rnd is False or rnd == "f32":
+        return lambda a: np.asarray(a, dtype=np.float32)
+    raise ValueError(f"rounding mode {rnd!r}")
+
+
+def norm_rope(x, w, cos, sin, eps: float, rnd):
     """x [S, H, D], w [D], cos / sin [S, D] (values already in the model dtype).
+    rnd: the model dtype's rounding, "bf16" (or True), "f16", "f32" (or False).
 
     Returns (out [S, H, D] fp32 holding model-dtype values, r [S, H] fp32)."""
-    T = _rounder(bf16)
+    T = _rounder(rnd)
     x = np.asarray(x, dtype=np.float32)
     S, H, D = x.shape
     half = D // 2

@@ -94,3 +94,36 @@ def torch_dense_reference(q, kfull, vfull, allowed, scale, do=None, grad_start=0
             dk[g] += kh.grad[grad_start:]
             dv[g] += vh.grad[grad_start:]
     return o, lse, dq, dk, dv
+
+
+def round_to(dtype):
+    """fp64 -> the values of a 16-bit torch dtype, as fp64 (round to nearest even)."""
+    return lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dtype).double().numpy()
+
+
+def rounding_model_grad_errors(q, k, v, do, allowed, scale, grad_start, rnd):
+    """Error against float64 of attention gradients computed with only the
+    reference's 16-bit rounding points (its compiled flex kernels cast P to the
+    operand dtype before dV = P^T dO, and dS before dQ and dK), everything else
+    in float64. Returns {name: (max-abs, mean-abs)} for dq, dk, dv: the error
+    floor of any implementation with those rounding points on these inputs."""
+    o, lse = mo.attention_fwd(q, k, v, allowed, scale)
+    exact = mo.attention_bwd(q, k, v, o, lse, do, allowed, scale, grad_start=grad_start)
+    Hq, S, D = q.shape
+    Hkv, L, _ = k.shape
+    G = Hq // Hkv
+    dq = np.zeros((Hq, S, D))
+    dk = np.zeros((Hkv, L, D))
+    dv = np.zeros((Hkv, L, D))
+    for h in range(Hq):
+        g = h // G
+        s = scale * (q[h] @ k[g].T)
+        rowok = np.isfinite(lse[h])
+        p = np.where(allowed & rowok[:, None], np.exp(s - np.where(rowok, lse[h], 0.0)[:, None]), 0.0)
+        dv[g] += rnd(p).T @ do[h]
+        ds = rnd(p * (do[h] @ v[g].T - (o[h] * do[h]).sum(axis=1)[:, None]))
+        dq[h] = scale * (ds @ k[g])
+        dk[g] += scale * (ds.T @ q[h])
+    got = (dq, dk[:, grad_start:], dv[:, grad_start:])
+    return {n: (float(np.abs(a - b).max()), float(np.abs(a - b).mean()))
+            for n, a, b in zip(("dq", "dk", "dv"), got, exact)}

@@ -1,24 +1,30 @@
 """HIP MTP attention forward/backward against the float64 CPU oracle (small
 and medium shapes) and an fp32 torch dense reference on the GPU (full config
-sizes). Tolerance: max-abs <= 2e-2, mean-abs <= 2e-3 on outputs and on every
-gradient; LSE within the same bounds; cache contents bit-exact."""
+sizes). Tolerance (bf16 operands): max-abs <= 2e-2, mean-abs <= 2e-3 on
+outputs and on every gradient; LSE within the same bounds; cache contents
+bit-exact. fp16 operands (three more mantissa bits than bf16, so every
+rounding the kernels share with the reference's flex path -- the
+probabilities and dS before their products, the outputs -- is 8x smaller):
+max-abs <= 4e-3, mean-abs <= 4e-4, gradients with the max bound relative
+above magnitude 1."""
 import numpy as np
 import pytest
 import torch
 
-from gpu_helpers import MAX_ABS, MEAN_ABS, check, chunk_layout, f64, qkv, torch_dense_reference
+from gpu_helpers import (MAX_ABS, MEAN_ABS, check, chunk_layout, f64, qkv, round_to,
+                         rounding_model_grad_errors, torch_dense_reference)
 from oracle import mtp_oracle as mo
 
 pytestmark = pytest.mark.gpu
 
 
 def run_case(mga, dev, n_reg, n_anchor, draft, P, Hq, Hkv, D, dtype=torch.bfloat16, seed=0,
-             pad=0, tail=False, every=None, use_cache=True):
+             pad=0, tail=False, every=None, use_cache=True, std=0.5):
     print(f"case n_reg={n_reg} anchors={n_anchor} draft={draft} P={P} Hq={Hq} Hkv={Hkv} D={D} "
-          f"{dtype} pad={pad} tail={tail} cache={use_cache}", flush=True)
+          f"{dtype} pad={pad} tail={tail} cache={use_cache} std={std}", flush=True)
     seq = chunk_layout(n_reg, n_anchor, draft, P, seed=seed, pad=pad, tail=tail, every=every)
     S = len(seq.gate)
-    q, k, v, kp, vp, do = qkv(S, P, Hq, Hkv, D, dtype, dev, seed=seed)
+    q, k, v, kp, vp, do = qkv(S, P, Hq, Hkv, D, dtype, dev, seed=seed, std=std)
     q.requires_grad_()
     k.requires_grad_()
     v.requires_grad_()
@@ -37,22 +43,28 @@ def run_case(mga, dev, n_reg, n_anchor, draft, P, Hq, Hkv, D, dtype=torch.bfloat
     return seq, q, k, v, kp, vp, do, o, lse
 
 
-def compare_oracle(seq, P, q, k, v, kp, vp, do, o, lse, D, grad_start):
+F16_MAX_ABS = 4e-3
+F16_MEAN_ABS = 4e-4
+
+
+def compare_oracle(seq, P, q, k, v, kp, vp, do, o, lse, D, grad_start, max_abs=MAX_ABS, mean_abs=MEAN_ABS,
+                   grad_scaled=False):
     allowed = mo.mtp_mask_dense(seq.gate, P)
     qn = f64(q)[0]
     kn = np.concatenate([f64(kp)[0], f64(k)[0]], axis=1)
     vn = np.concatenate([f64(vp)[0], f64(v)[0]], axis=1)
     on, lsen = mo.attention_fwd(qn, kn, vn, allowed, D ** -0.5)
-    check("o", f64(o)[0].transpose(1, 0, 2), on)
+    tol = dict(max_abs=max_abs, mean_abs=mean_abs)
+    check("o", f64(o)[0].transpose(1, 0, 2), on, **tol)
     got_lse = f64(lse)[0]
     assert np.array_equal(np.isneginf(got_lse), np.isneginf(lsen))
     fin = np.isfinite(lsen)
-    check("lse", got_lse[fin], lsen[fin])
+    check("lse", got_lse[fin], lsen[fin], **tol, scale_above_one=grad_scaled)
     dqn, dkn, dvn = mo.attention_bwd(qn, kn, vn, on, lsen, f64(do)[0].transpose(1, 0, 2),
                                      allowed, D ** -0.5, grad_start=grad_start)
-    check("dq", f64(q.grad)[0], dqn)
-    check("dk", f64(k.grad)[0], dkn[:, -k.shape[2]:])
-    check("dv", f64(v.grad)[0], dvn[:, -v.shape[2]:])
+    check("dq", f64(q.grad)[0], dqn, **tol, scale_above_one=grad_scaled)
+    check("dk", f64(k.grad)[0], dkn[:, -k.shape[2]:], **tol, scale_above_one=grad_scaled)
+    check("dv", f64(v.grad)[0], dvn[:, -v.shape[2]:], **tol, scale_above_one=grad_scaled)
 
 
 SMALL = [
@@ -73,6 +85,55 @@ def test_attention_small_bf16(mga, dev, c):
     out = run_case(mga, dev, **c)
     seq, q, k, v, kp, vp, do, o, lse = out
     compare_oracle(seq, c["P"], q, k, v, kp, vp, do, o, lse, c["D"], grad_start=c["P"])
+
+
+@pytest.mark.parametrize("c", SMALL)
+def test_attention_small_fp16(mga, dev, c):
+    """fp16 operands run the fp16 MFMAs (probabilities and dS rounded to
+    fp16, as the reference's flex kernels round them to the operand dtype)."""
+    seq, q, k, v, kp, vp, do, o, lse = run_case(mga, dev, dtype=torch.float16, seed=3, **c)
+    assert o.dtype == torch.float16 and q.grad.dtype == torch.float16 and k.grad.dtype == torch.float16
+    compare_oracle(seq, c["P"], q, k, v, kp, vp, do, o, lse, c["D"], grad_start=c["P"],
+                   max_abs=F16_MAX_ABS, mean_abs=F16_MEAN_ABS, grad_scaled=True)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_attention_large_logits(mga, dev, dtype):
+    """q, k ~ N(0, 2^2): scaled scores spread over tens of log2 units, so the
+    forward's lazy softmax offset keeps leaving its bound (2^15 per
+    probability for fp16, whose largest finite is 65504; 2^20 for bf16) and
+    the exact-max recomputation runs on many steps. Outputs and LSE: the
+    dtype's standard bounds, relative above magnitude 1 (v ~ N(0, 2^2) puts
+    outputs near 6, where one bf16 rounding is 1.6e-2). Gradients grow to |dq| ~ 13 here and dS to tens
+    of units, so the 16-bit roundings of P and dS alone (the reference's
+    rounding points) cost more than the O(1)-scale bounds: each gradient must
+    stay within 3x the max- and mean-abs error of that rounding model
+    (rounding_model_grad_errors) on the same inputs; the factor covers this
+    kernel's further roundings (outputs, the LSE summed from rounded
+    probabilities, delta from the stored output)."""
+    c = dict(n_reg=320, n_anchor=24, draft=4, P=192, Hq=4, Hkv=2, D=128)
+    seq, q, k, v, kp, vp, do, o, lse = run_case(mga, dev, dtype=dtype, seed=11, std=2.0, **c)
+    P, D = c["P"], c["D"]
+    lse_np = f64(lse)[0]
+    print(f"  lse range {lse_np[np.isfinite(lse_np)].min():.1f} .. {lse_np.max():.1f}", flush=True)
+    tol = dict(max_abs=F16_MAX_ABS, mean_abs=F16_MEAN_ABS) if dtype == torch.float16 else \
+        dict(max_abs=MAX_ABS, mean_abs=MEAN_ABS)
+    allowed = mo.mtp_mask_dense(seq.gate, P)
+    qn = f64(q)[0]
+    kn = np.concatenate([f64(kp)[0], f64(k)[0]], axis=1)
+    vn = np.concatenate([f64(vp)[0], f64(v)[0]], axis=1)
+    don = f64(do)[0].transpose(1, 0, 2)
+    on, lsen = mo.attention_fwd(qn, kn, vn, allowed, D ** -0.5)
+    check("o", f64(o)[0].transpose(1, 0, 2), on, **tol, scale_above_one=True)
+    fin = np.isfinite(lsen)
+    assert np.array_equal(np.isneginf(lse_np), np.isneginf(lsen))
+    check("lse", lse_np[fin], lsen[fin], **tol, scale_above_one=True)
+    dqn, dkn, dvn = mo.attention_bwd(qn, kn, vn, on, lsen, don, allowed, D ** -0.5, grad_start=P)
+    model = rounding_model_grad_errors(qn, kn, vn, don, allowed, D ** -0.5, P, round_to(dtype))
+    for name, got, ref in (("dq", q.grad, dqn), ("dk", k.grad, dkn), ("dv", v.grad, dvn)):
+        mx, mn = model[name]
+        print(f"  {name} rounding model: max-abs {mx:.3e} mean-abs {mn:.3e}", flush=True)
+        check(name, f64(got)[0], ref, max_abs=3 * mx, mean_abs=3 * mn)
 
 
 @pytest.mark.parametrize("D", [64, 128])
@@ -129,18 +190,29 @@ def test_attention_full_config(mga, dev, cfg):
     """Full attention geometry of Qwen3-8B / Llama-3.1-8B (32 q / 8 kv heads,
     D = 128) against an fp32 dense reference on the GPU fed the same bf16
     values, up to config 4's 131 072-token cache."""
+    full_config_case(mga, dev, cfg, torch.bfloat16)
+
+
+def test_attention_full_config_fp16(mga, dev):
+    """Config 2's geometry with fp16 operands, fp16 bounds."""
+    full_config_case(mga, dev, dict(n_reg=4096, n_anchor=256, draft=4, P=8192), torch.float16,
+                     max_abs=F16_MAX_ABS, mean_abs=F16_MEAN_ABS, grad_scaled=True)
+
+
+def full_config_case(mga, dev, cfg, dtype, max_abs=MAX_ABS, mean_abs=MEAN_ABS, grad_scaled=False):
     Hq, Hkv, D = 32, 8, 128
     seq, q, k, v, kp, vp, do, o, lse = run_case(
         mga, dev, cfg["n_reg"], cfg["n_anchor"], cfg["draft"], cfg["P"], Hq, Hkv, D, seed=2,
-        every=cfg.get("every"))
+        every=cfg.get("every"), dtype=dtype)
     P = cfg["P"]
     allowed = mo.mtp_mask_dense(seq.gate, P)
     kfull = torch.cat([kp, k.detach()], dim=2)
     vfull = torch.cat([vp, v.detach()], dim=2)
     ro, rlse, rdq, rdk, rdv = torch_dense_reference(q.detach(), kfull, vfull, allowed, D ** -0.5,
                                                     do=do, grad_start=P)
-    check("o", f64(o)[0].transpose(1, 0, 2), ro.cpu().numpy())
-    check("lse", f64(lse)[0], rlse.cpu().numpy())
-    check("dq", f64(q.grad)[0], rdq.cpu().numpy())
-    check("dk", f64(k.grad)[0], rdk.cpu().numpy())
-    check("dv", f64(v.grad)[0], rdv.cpu().numpy())
+    tol = dict(max_abs=max_abs, mean_abs=mean_abs)
+    check("o", f64(o)[0].transpose(1, 0, 2), ro.cpu().numpy(), **tol)
+    check("lse", f64(lse)[0], rlse.cpu().numpy(), **tol, scale_above_one=grad_scaled)
+    check("dq", f64(q.grad)[0], rdq.cpu().numpy(), **tol, scale_above_one=grad_scaled)
+    check("dk", f64(k.grad)[0], rdk.cpu().numpy(), **tol, scale_above_one=grad_scaled)
+    check("dv", f64(v.grad)[0], rdv.cpu().numpy(), **tol, scale_above_one=grad_scaled)

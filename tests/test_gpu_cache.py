@@ -12,7 +12,7 @@ from oracle import mtp_oracle as mo
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("D", [64, 128])
 def test_kv_append_identity_and_gather(mga, dev, dtype, D):
     torch.manual_seed(0)

@@ -7,10 +7,11 @@ Forward tolerance (bf16): the kernel rounds after every op exactly where the
 reference does, so outputs are bit-equal except where the fp32 row mean or the
 hardware rsqrt differs from the checker's in the last fp32 bit and flips one
 bf16 rounding: at most 1e-3 of the elements differ, each by at most 2^-6 of
-its row's largest magnitude. fp32: rtol 1e-5, atol 1e-6. rstd: rtol 2e-6.
-Backward: the oracle's float64 gradient on the same bf16 inputs; each bf16
-element within 2^-8 of its value plus 1e-5 of the tensor's largest (one bf16
-rounding of an fp32 result); fp32 within 1e-5 relative.
+its row's largest magnitude (fp16: the same fraction, 2^-9). fp32: rtol 1e-5,
+atol 1e-6. rstd: rtol 2e-6. Backward: the oracle's float64 gradient on the
+same inputs; each bf16 element within 2^-8 of its value plus 1e-5 of the
+tensor's largest (one bf16 rounding of an fp32 result), fp16 within 2^-11
+plus the same; fp32 within 1e-5 relative.
 """
 import numpy as np
 import pytest
@@ -44,7 +45,7 @@ def oracle_fwd(q, k, qw, kw, cos, sin, eps, bf16):
     return qo, ko, np.concatenate([qr_, kr_], axis=1)
 
 
-def check_bf16(name, got, ref):
+def check_bf16(name, got, ref, bound=2.0 ** -6):
     diff = got != ref
     frac = diff.mean()
     rowmax = np.abs(ref).max(axis=-1, keepdims=True)
@@ -52,7 +53,7 @@ def check_bf16(name, got, ref):
     print(f"  {name}: {diff.sum()} of {diff.size} differ ({frac:.2e}), max {err.max():.2e} of row max",
           flush=True)
     assert frac <= 1e-3, name
-    assert err.max() <= 2.0 ** -6, name
+    assert err.max() <= bound, name
 
 
 def run_fwd(mga, q, k, qw, kw, cos, sin, eps=1e-6):
@@ -71,6 +72,17 @@ def test_forward_bf16_against_oracle(mga, dev, S, Hq, Hkv, D):
     rq, rk, rr = oracle_fwd(q, k, qw, kw, cos, sin, 1e-6, True)
     check_bf16("q", npf(qo)[0], rq)
     check_bf16("k", npf(ko)[0], rk)
+    np.testing.assert_allclose(npf(rstd), rr, rtol=2e-6)
+
+
+@pytest.mark.parametrize("S,Hq,Hkv,D", [(1024, 32, 8, 128), (65, 6, 3, 96), (33, 2, 1, 80), (5, 1, 1, 2)])
+def test_forward_fp16_against_oracle(mga, dev, S, Hq, Hkv, D):
+    q, k, qw, kw, cos, sin = make(S, Hq, Hkv, D, torch.float16, dev, seed=S + 2, pos0=4096)
+    qo, ko, rstd = run_fwd(mga, q, k, qw, kw, cos, sin)
+    assert qo.dtype == torch.float16 and ko.dtype == torch.float16
+    rq, rk, rr = oracle_fwd(q, k, qw, kw, cos, sin, 1e-6, "f16")
+    check_bf16("q", npf(qo)[0], rq, bound=2.0 ** -9)
+    check_bf16("k", npf(ko)[0], rk, bound=2.0 ** -9)
     np.testing.assert_allclose(npf(rstd), rr, rtol=2e-6)
 
 
@@ -120,7 +132,7 @@ def test_strided_fused_projection_and_misaligned(mga, dev):
     check_bf16("misaligned q", npf(qo)[0], rq)
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("S,Hq,Hkv,D", [(512, 32, 8, 128), (65, 6, 3, 96), (17, 4, 2, 64)])
 def test_backward_against_oracle(mga, dev, dtype, S, Hq, Hkv, D):
     q, k, qw, kw, cos, sin = make(S, Hq, Hkv, D, dtype, dev, seed=S + 1)
@@ -140,6 +152,8 @@ def test_backward_against_oracle(mga, dev, dtype, S, Hq, Hkv, D):
         print(f"  {dtype} {name}: max-abs {err.max():.3e} (scale {scale:.3e})", flush=True)
         if dtype == torch.bfloat16:
             assert (err <= 2.0 ** -8 * np.abs(ref) + 1e-5 * scale).all(), name
+        elif dtype == torch.float16:
+            assert (err <= 2.0 ** -11 * np.abs(ref) + 1e-5 * scale).all(), name
         else:
             assert (err <= 1e-5 * np.abs(ref) + 1e-6 * scale).all(), name
 

@@ -7,6 +7,9 @@
 * bf16 logits (the model dtype) at the sampler's shape, V = 151936: the oracle
   runs on the same bf16 values; loss within rtol 1e-4, gradient (bf16) within
   one bf16 rounding of the oracle's value (rtol 2^-7) plus atol 1e-7.
+* fp16 logits at the same shape: loss within rtol 1e-4, gradient (fp16)
+  within 2^-10 of the oracle's value plus 3e-8 (half the spacing of fp16's
+  subnormals, where most of the gradient's elements lie).
 * A strided teacher (the reference's call site passes a strided view,
   core/mtp.py:124), widths that are not multiples of the vector width, a
   misaligned row stride (element-load path), a single column, and rows whose
@@ -61,6 +64,22 @@ def test_bf16_sampler_shape(mga, dev, rows):
     err = np.abs(_f64(grad) - ref_g)
     print(f"  rows {rows}: loss {loss:.4f} ref {ref:.4f} grad max-abs {err.max():.3e}", flush=True)
     assert (err <= 2.0 ** -7 * np.abs(ref_g) + 1e-7).all()
+
+
+@pytest.mark.parametrize("rows", [1, 300])
+def test_fp16_sampler_shape(mga, dev, rows):
+    g = torch.Generator(device=dev).manual_seed(rows + 7)
+    V = 151936
+    x = (torch.randn(1, rows, V, generator=g, device=dev) * 3).half()
+    t = (torch.randn(1, rows, V, generator=g, device=dev) * 3).half()
+    loss, grad = _run(mga, x, t, go=0.5)
+    ref = sc.soft_ce_loss(_f64(x), _f64(t))
+    ref_g = 0.5 * sc.soft_ce_grad(_f64(x), _f64(t))
+    assert abs(loss - ref) <= 1e-4 * abs(ref)
+    assert grad.dtype == torch.float16
+    err = np.abs(_f64(grad) - ref_g)
+    print(f"  rows {rows}: loss {loss:.4f} ref {ref:.4f} grad max-abs {err.max():.3e}", flush=True)
+    assert (err <= 2.0 ** -10 * np.abs(ref_g) + 3e-8).all()
 
 
 def test_strided_teacher_and_odd_widths(mga, dev):

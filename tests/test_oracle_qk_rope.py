@@ -60,6 +60,30 @@ def test_bf16_matches_library_ops(D):
     assert np.abs(got - ref).max() <= 2.0 ** -6 * scale
 
 
+@pytest.mark.parametrize("D", [128, 64])
+def test_f16_matches_library_ops(D):
+    x, w, cos, sin = _inputs(96, 12, D, D + 1, torch.float16)
+    ref = _library(x, w, cos, sin, 1e-6)
+    got, _ = _oracle(x, w, cos, sin, 1e-6, "f16")
+    diff = got != ref
+    assert diff.mean() < 1e-3, diff.mean()
+    assert np.abs(got - ref).max() <= 2.0 ** -9 * np.abs(ref).max()
+    # the bf16 rounding in its place is caught
+    wrong, _ = _oracle(x, w, cos, sin, 1e-6, "bf16")
+    assert (wrong != ref).mean() > 0.1
+
+
+def test_f16_round_known_values():
+    vals = np.array([1.0, 1.0 + 2.0 ** -11, 1.0 + 3 * 2.0 ** -11, 65504.0, 65520.0, 2.0 ** -25, 2.0 ** -24 * 1.5,
+                     -3.0e-5], dtype=np.float32)
+    want = np.array([1.0, 1.0, 1.0 + 2.0 ** -9, 65504.0, np.inf, 0.0, 2.0 ** -23, -3.0e-5], dtype=np.float32)
+    got = qr.f16_round(vals)
+    np.testing.assert_array_equal(got[:7], want[:7])
+    assert abs(got[7] - want[7]) <= 2.0 ** -25   # a subnormal: spacing 2^-24
+    a = np.random.default_rng(1).standard_normal(4096).astype(np.float32) * 100
+    np.testing.assert_array_equal(qr.f16_round(a), torch.tensor(a).half().float().numpy())
+
+
 def test_dropped_roundings_are_caught():
     x, w, cos, sin = _inputs(64, 8, 128, 5, torch.bfloat16)
     ref = _library(x, w, cos, sin, 1e-6)
