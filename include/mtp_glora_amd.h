@@ -18,7 +18,7 @@
  *     model dtype). Attention arithmetic: bf16 operands run bf16 MFMAs and
  *     fp16 operands fp16 MFMAs, with fp32 accumulation and the probabilities
  *     and dS rounded to the operand type before their products; fp32
- *     operands are rounded to bf16 for the MFMAs.
+ *     operands run fp32 MFMAs (fp32 products, softmax and gradients).
  *   - the MTP mask is carried by one int32 code per chunk token:
  *       -1 pad, -2 regular token (x), >= 0 mask token (m) = its
  *       num_prefix_x value; every cached prefix key counts as x.

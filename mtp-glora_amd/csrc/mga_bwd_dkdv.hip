@@ -61,48 +61,25 @@ __device__ __forceinline__ f32x16 rows16(const float *t, uint32_t ofs) {
   return v;
 }
 
-// Global -> LDS staging of a 32 x HD tile by the 4 waves of a group (w4:
-// the wave within the group, gt: the thread within the group); rows past
-// rmax repeat row rmax. bf16: direct loads (completion on vmcnt); fp32:
-// through registers, converted to bf16 at store time.
-template <int HD, typename T>
+// Global -> LDS staging of a 32 x HD tile (bf16 or fp16) by the 4 waves of a
+// group (w4: the wave within the group, gt: the thread within the group):
+// direct loads, completion on vmcnt; rows past rmax repeat row rmax.
+template <int HD>
 struct GroupTile {
-  static constexpr int kGran = kRows * HD / 8 / 256;
-  static constexpr int kInst = kRows / (64 / (HD / 8)) / 4;   // direct loads per wave (bf16)
-  i32x4 reg[sizeof(T) == 2 ? 1 : kGran];
+  static constexpr int kGranRow = HD / 8;
+  static constexpr int kRowsPerInst = 64 / kGranRow;
+  static constexpr int kInst = kRows / kRowsPerInst / 4;   // direct loads per wave
 
-  __device__ __forceinline__ void load(bf16_t *tile, const T *src, int64_t ss, int r0, int rmax, int w4, int gt) {
-    if constexpr (sizeof(T) == 2) {
-      constexpr int kGranRow = HD / 8;
-      constexpr int kRowsPerInst = 64 / kGranRow;
-      constexpr int kInst = kRows / kRowsPerInst / 4;
-      const int lane = gt & 63, p = lane % kGranRow;
+  __device__ __forceinline__ static void load(bf16_t *tile, const bf16_t *src, int64_t ss, int r0, int rmax,
+                                              int w4, int gt) {
+    const int lane = gt & 63, p = lane % kGranRow;
 #pragma unroll
-      for (int i = 0; i < kInst; ++i) {
-        const int blk = w4 * kInst + i;
-        const int r = blk * kRowsPerInst + lane / kGranRow;
-        const int c = p ^ swz<HD>(r);
-        const int row = min(r0 + r, rmax);
-        __builtin_amdgcn_global_load_lds(reinterpret_cast<const bf16_t *>(src) + (int64_t)row * ss + c * 8,
-                                         (lds_void *)(tile + blk * 512), 16, 0, 0);
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < kGran; ++i) {
-        const int gi = gt + 256 * i;
-        const int r = gi / (HD / 8), c = gi % (HD / 8);
-        reg[i] = __builtin_bit_cast(i32x4, load8(src + (int64_t)min(r0 + r, rmax) * ss + c * 8));
-      }
-    }
-  }
-  __device__ __forceinline__ void store(bf16_t *tile, int gt) const {
-    if constexpr (sizeof(T) != 2) {
-#pragma unroll
-      for (int i = 0; i < kGran; ++i) {
-        const int gi = gt + 256 * i;
-        const int r = gi / (HD / 8), c = gi % (HD / 8);
-        *reinterpret_cast<i32x4 *>(tile + tile_off<HD>(r, c)) = reg[i];
-      }
+    for (int i = 0; i < kInst; ++i) {
+      const int blk = w4 * kInst + i;
+      const int r = blk * kRowsPerInst + lane / kGranRow;
+      const int c = p ^ swz<HD>(r);
+      const int row = min(r0 + r, rmax);
+      __builtin_amdgcn_global_load_lds(src + (int64_t)row * ss + c * 8, (lds_void *)(tile + blk * 512), 16, 0, 0);
     }
   }
 };
@@ -199,24 +176,16 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_kernel(AttnArgs a, 
   const float c = a.scale_log2;
   const float inv_scale = 1.f / a.scale;
 
-  // tiles: global -> LDS two steps ahead (fp32: through one of two register
-  // slots); row data: global -> registers at the start of the step before
-  // its own, -> LDS at that step's end
-  GroupTile<HD, T> stQ[2], stD[2];
+  // tiles: global -> LDS two steps ahead; row data: global -> registers at
+  // the start of the step before its own, -> LDS at that step's end
   float rl = 0.f, re = 0.f;
   int rc = kCodePad, rq = 0;
-  auto load_tiles = [&](const StepInfo &s, bf16_t *dQ, bf16_t *dD, int slot) {
+  auto load_tiles = [&](const StepInfo &s, bf16_t *dQ, bf16_t *dD) {
     if (s.flags & 1) {
-      const T *qp = reinterpret_cast<const T *>(a.q) + s.h * a.q_sh;
-      const T *dop = reinterpret_cast<const T *>(a.dout) + s.h * a.do_sh;
-      stQ[slot].load(dQ, qp, a.q_ss, s.q0, a.S - 1, w4, gt);
-      stD[slot].load(dD, dop, a.do_ss, s.q0, a.S - 1, w4, gt);
-    }
-  };
-  auto store_tiles = [&](const StepInfo &s, bf16_t *dQ, bf16_t *dD, int slot) {
-    if (s.flags & 1) {
-      stQ[slot].store(dQ, gt);
-      stD[slot].store(dD, gt);
+      const bf16_t *qp = reinterpret_cast<const bf16_t *>(a.q) + s.h * a.q_sh;
+      const bf16_t *dop = reinterpret_cast<const bf16_t *>(a.dout) + s.h * a.do_sh;
+      GroupTile<HD>::load(dQ, qp, a.q_ss, s.q0, a.S - 1, w4, gt);
+      GroupTile<HD>::load(dD, dop, a.do_ss, s.q0, a.S - 1, w4, gt);
     }
   };
   auto load_rows = [&](const StepInfo &s) {
@@ -274,11 +243,10 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_kernel(AttnArgs a, 
   ring[0] = info_of(0);
   ring[1] = info_of(1);
   load_rows(ring[0]);
-  load_tiles(ring[0], sQ0 + gr * TILE, sD0 + gr * TILE, 0);
+  load_tiles(ring[0], sQ0 + gr * TILE, sD0 + gr * TILE);
   __builtin_amdgcn_s_waitcnt(0);   // this thread's loads of step 0 landed
-  store_tiles(ring[0], sQ0 + gr * TILE, sD0 + gr * TILE, 0);
   store_rows(ring[0], sL0 + gr * kRows, sE0 + gr * kRows, sC0 + gr * kRows);
-  load_tiles(ring[1], sQ1 + gr * TILE, sD1 + gr * TILE, 1);
+  load_tiles(ring[1], sQ1 + gr * TILE, sD1 + gr * TILE);
   __syncthreads();
 
   // B: dP - delta of the current and the previous step, alternating by step parity
@@ -307,7 +275,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_kernel(AttnArgs a, 
     StepInfo nxt2{0, 0, 0};
     if (j + 2 < nsteps) {
       nxt2 = info_of(j + 2);
-      load_tiles(nxt2, qb((J + 2) % 4) + gr * TILE, db_((J + 2) % 4) + gr * TILE, J % 2);
+      load_tiles(nxt2, qb((J + 2) % 4) + gr * TILE, db_((J + 2) % 4) + gr * TILE);
     }
 
     // The products run on every step, inactive ones included (the operands are
@@ -396,12 +364,9 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_kernel(AttnArgs a, 
     if (j + 1 < nsteps) {
       // this thread's loads of step j + 1 landed (issued one step ago): wait
       // for all but the tiles of step j + 2 just issued
-      if constexpr (sizeof(T) == 2) {
-        constexpr int n = 2 * GroupTile<HD, T>::kInst;
-        if (nxt2.flags & 1) __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8));
-        else __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));   // vmcnt(0)
-      }
-      store_tiles(nxt1, qb((J + 1) % 4) + gr * TILE, db_((J + 1) % 4) + gr * TILE, (J + 1) % 2);
+      constexpr int n = 2 * GroupTile<HD>::kInst;
+      if (nxt2.flags & 1) __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8));
+      else __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));   // vmcnt(0)
       store_rows(nxt1, lb((J + 1) % 2) + gr * kRows, eb((J + 1) % 2) + gr * kRows, cb((J + 1) % 2) + gr * kRows);
     }
     ring[(J + 2) % 4] = nxt2;
@@ -481,13 +446,13 @@ static void bwd_launch(const AttnArgs &a, int passes, hipStream_t st) {
 
 template <int HD>
 static void bwd_launch_dt(const AttnArgs &a, int dtype, int passes, hipStream_t st) {
-  if (dtype == kDtF32) bwd_launch<HD, float>(a, passes, st);
-  else if (dtype == kDtF16) bwd_launch<HD, f16_t>(a, passes, st);
+  if (dtype == kDtF16) bwd_launch<HD, f16_t>(a, passes, st);
   else bwd_launch<HD, bf16_t>(a, passes, st);
 }
 
 void launch_attn_bwd(const AttnArgs &a, int head_dim, int dtype, int passes, hipStream_t st) {
-  if (head_dim == 128) bwd_launch_dt<128>(a, dtype, passes, st);
+  if (dtype == kDtF32) launch_attn_bwd_f32(a, head_dim, passes, st);
+  else if (head_dim == 128) bwd_launch_dt<128>(a, dtype, passes, st);
   else bwd_launch_dt<64>(a, dtype, passes, st);
 }
 

@@ -33,17 +33,10 @@ __device__ __forceinline__ float half_row_dot(const T *o, const T *d, int hi) {
 #pragma unroll
   for (int ks = 0; ks < HD / 16; ++ks) {
     const int c = ks * 16 + hi * 8;
-    if constexpr (sizeof(T) == 2) {
-      const auto x = __builtin_bit_cast(typename Elem<T>::v8, load8(o + c));
-      const auto y = __builtin_bit_cast(typename Elem<T>::v8, load8(d + c));
+    const auto x = __builtin_bit_cast(typename Elem<T>::v8, load8(o + c));
+    const auto y = __builtin_bit_cast(typename Elem<T>::v8, load8(d + c));
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc += (float)x[e] * (float)y[e];
-    } else {
-      const f32x4 x0 = *reinterpret_cast<const f32x4 *>(o + c), x1 = *reinterpret_cast<const f32x4 *>(o + c + 4);
-      const f32x4 y0 = *reinterpret_cast<const f32x4 *>(d + c), y1 = *reinterpret_cast<const f32x4 *>(d + c + 4);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) acc += x0[e] * y0[e] + x1[e] * y1[e];
-    }
+    for (int e = 0; e < 8; ++e) acc += (float)x[e] * (float)y[e];
   }
   return acc;
 }
@@ -120,31 +113,18 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnArgs a) {
   TrOffsets<HD> tro;
   tro.init(lane);
 
-  // bf16 operands go global -> LDS directly (no staging registers); fp32
-  // operands are converted through registers.
-  constexpr bool kDirect = sizeof(T) == 2;
-  TileStage<HD, kDirect ? 0 : kStep, T> stK, stV;
+  // K/V tiles go global -> LDS directly (no staging registers)
   KeyCode knext;
   auto load_step = [&](int j, bf16_t *dK, bf16_t *dV) {
     const int kb = step_base(j);
-    if constexpr (kDirect) {
-      if (kb < a.L) {   // a step past the keys is never computed: nothing to load
-        tile_dma<HD, kStep>(dK, reinterpret_cast<const bf16_t *>(kp), a.k_ss, kb, a.L - 1);
-        tile_dma<HD, kStep>(dV, reinterpret_cast<const bf16_t *>(vp), a.v_ss, kb, a.L - 1);
-      }
-    } else {
-      stK.load(kp, a.k_ss, kb, a.L - 1);
-      stV.load(vp, a.v_ss, kb, a.L - 1);
+    if (kb < a.L) {   // a step past the keys is never computed: nothing to load
+      tile_dma<HD, kStep>(dK, reinterpret_cast<const bf16_t *>(kp), a.k_ss, kb, a.L - 1);
+      tile_dma<HD, kStep>(dV, reinterpret_cast<const bf16_t *>(vp), a.v_ss, kb, a.L - 1);
     }
     if (tid < kStep) knext.load(a.code, kb + tid, a.P, a.L);   // converted at store time
   };
-  auto store_step = [&](bf16_t *dK, bf16_t *dV, int *dW) {
-    if constexpr (!kDirect) {
-      stK.store(dK);
-      stV.store(dV);
-    } else {
-      __builtin_amdgcn_s_waitcnt(0);   // this thread's direct loads have landed
-    }
+  auto store_step = [&](bf16_t *, bf16_t *, int *dW) {
+    __builtin_amdgcn_s_waitcnt(0);   // this thread's direct loads have landed
     if (tid < kStep) *reinterpret_cast<int *>(const_cast<char *>(lds_at(dW, opaque_u32(tid * 4u)))) = knext.w();
   };
 
@@ -254,9 +234,7 @@ void dq_launch(const AttnArgs &a, hipStream_t st) {
 }
 
 template void dq_launch<128, bf16_t>(const AttnArgs &, hipStream_t);
-template void dq_launch<128, float>(const AttnArgs &, hipStream_t);
 template void dq_launch<64, bf16_t>(const AttnArgs &, hipStream_t);
-template void dq_launch<64, float>(const AttnArgs &, hipStream_t);
 template void dq_launch<128, f16_t>(const AttnArgs &, hipStream_t);
 template void dq_launch<64, f16_t>(const AttnArgs &, hipStream_t);
 

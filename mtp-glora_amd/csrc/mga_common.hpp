@@ -38,15 +38,6 @@ __device__ __forceinline__ bf16x8 load8(const f16_t *p) {
   return __builtin_bit_cast(bf16x8, *reinterpret_cast<const i32x4 *>(p));
 }
 
-__device__ __forceinline__ bf16x8 load8(const float *p) {
-  const f32x4 a = *reinterpret_cast<const f32x4 *>(p);
-  const f32x4 b = *reinterpret_cast<const f32x4 *>(p + 4);
-  bf16x8 r;
-  r[0] = (bf16_t)a[0]; r[1] = (bf16_t)a[1]; r[2] = (bf16_t)a[2]; r[3] = (bf16_t)a[3];
-  r[4] = (bf16_t)b[0]; r[5] = (bf16_t)b[1]; r[6] = (bf16_t)b[2]; r[7] = (bf16_t)b[3];
-  return r;
-}
-
 // ---- stores of 4 consecutive output values -------------------------------
 
 __device__ __forceinline__ void store4(bf16_t *p, float a, float b, float c, float d) {
@@ -138,9 +129,9 @@ __device__ __forceinline__ f32x16 mfma32<f16_t>(bf16x8 a, bf16x8 b, f32x16 c) {
                                                 0, 0);
 }
 
-// The MFMA element of a storage type: fp16 data computes in fp16, bf16 data
-// in bf16 (fp32 data does not use these kernels).
-template <typename T> struct MfmaElem { typedef bf16_t type; };
+// The MFMA element of a 16-bit storage type: itself.
+template <typename T> struct MfmaElem;
+template <> struct MfmaElem<bf16_t> { typedef bf16_t type; };
 template <> struct MfmaElem<f16_t> { typedef f16_t type; };
 
 __device__ __forceinline__ f32x16 zero16() {
@@ -281,34 +272,6 @@ __device__ __forceinline__ bf16x8 lds_tr_operand(const bf16_t *tile, const TrLan
   const bf16_t *p1 = tile + (k0 + t.row[1]) * HD + t.lo[1] + ((mblk ^ t.hi2[1]) << 5);
   return join8(lds_tr4(p0), lds_tr4(p1));
 }
-
-// ---- global -> register -> LDS staging of an NR x HD tile ------------------
-// 256 threads; thread t owns granules t, t + 256, ...; rows beyond rmax repeat
-// row rmax (their values are masked or unused).
-template <int HD, int NR, typename T>
-struct TileStage {
-  static constexpr int kGran = NR * HD / 8 / 256;
-  i32x4 reg[kGran > 0 ? kGran : 1];
-
-  __device__ __forceinline__ void load(const T *src, int64_t ss, int r0, int rmax) {
-#pragma unroll
-    for (int i = 0; i < kGran; ++i) {
-      const int gi = threadIdx.x + 256 * i;
-      const int r = gi / (HD / 8), c = gi % (HD / 8);
-      const int row = min(r0 + r, rmax);
-      reg[i] = __builtin_bit_cast(i32x4, load8(src + (int64_t)row * ss + c * 8));
-    }
-  }
-
-  __device__ __forceinline__ void store(bf16_t *tile) const {
-#pragma unroll
-    for (int i = 0; i < kGran; ++i) {
-      const int gi = threadIdx.x + 256 * i;
-      const int r = gi / (HD / 8), c = gi % (HD / 8);
-      *reinterpret_cast<i32x4 *>(tile + tile_off<HD>(r, c)) = reg[i];
-    }
-  }
-};
 
 }  // namespace mga
 

@@ -9,8 +9,8 @@
 // (plus one exchange with the lane 32 away) and accumulates O^T += V^T P^T,
 // feeding the probabilities from the accumulator registers straight into the
 // B operand. V^T comes from the row-major V tile through the LDS transpose
-// read. bf16 K/V tiles are loaded one step ahead straight into the other of
-// two named LDS buffers, so one barrier per step suffices.
+// read. K/V tiles (bf16 or fp16) are loaded one step ahead straight into the
+// other of two named LDS buffers, so one barrier per step suffices.
 //
 // NB = 1: 32 rows per wave, 2 waves per SIMD (256 registers each).
 // NB = 2: 64 rows per wave, 1 wave per SIMD; every K and V^T operand read from
@@ -116,42 +116,27 @@ __global__ __launch_bounds__(256, 3 - NB) void attn_fwd_kernel(AttnArgs a) {
   TrOffsets<HD> tro;
   tro.init(lane);
 
-  constexpr bool kDirect = sizeof(T) == 2;
   DmaLane<HD, kStepKeys> dma;   // shared by the K and V tiles
-  uint32_t lrowK = 0, lrowV = 0;
-  if constexpr (kDirect) {
-    dma.init();
-    lrowK = dma.lane_row(a.k_ss);
-    lrowV = dma.lane_row(a.v_ss);
-  }
-  TileStage<HD, kDirect ? 0 : kStepKeys, T> stK, stV;
+  dma.init();
+  const uint32_t lrowK = dma.lane_row(a.k_ss);
+  const uint32_t lrowV = dma.lane_row(a.v_ss);
   KeyCode wkey;
   auto load_step = [&](int j, bf16_t *dK, bf16_t *dV) {
     const int kb = step_base(j);
-    if constexpr (kDirect) {
-      if (kb >= a.L) {
-        // second half of the last tile, past the keys: never computed, nothing to load
-      } else if (kb + kStepKeys <= a.L) {
-        dma.issue(dK, reinterpret_cast<const bf16_t *>(kp) + (int64_t)kb * a.k_ss, a.k_ss, lrowK);
-        dma.issue(dV, reinterpret_cast<const bf16_t *>(vp) + (int64_t)kb * a.v_ss, a.v_ss, lrowV);
-      } else {
-        dma.issue_clamped(dK, reinterpret_cast<const bf16_t *>(kp) + (int64_t)kb * a.k_ss, a.k_ss, a.L - kb);
-        dma.issue_clamped(dV, reinterpret_cast<const bf16_t *>(vp) + (int64_t)kb * a.v_ss, a.v_ss, a.L - kb);
-      }
+    if (kb >= a.L) {
+      // second half of the last tile, past the keys: never computed, nothing to load
+    } else if (kb + kStepKeys <= a.L) {
+      dma.issue(dK, reinterpret_cast<const bf16_t *>(kp) + (int64_t)kb * a.k_ss, a.k_ss, lrowK);
+      dma.issue(dV, reinterpret_cast<const bf16_t *>(vp) + (int64_t)kb * a.v_ss, a.v_ss, lrowV);
     } else {
-      stK.load(kp, a.k_ss, kb, a.L - 1);
-      stV.load(vp, a.v_ss, kb, a.L - 1);
+      dma.issue_clamped(dK, reinterpret_cast<const bf16_t *>(kp) + (int64_t)kb * a.k_ss, a.k_ss, a.L - kb);
+      dma.issue_clamped(dV, reinterpret_cast<const bf16_t *>(vp) + (int64_t)kb * a.v_ss, a.v_ss, a.L - kb);
     }
     // raw code only: converting it here would wait for the tile loads too
     if (tid < kStepKeys) wkey.load(a.code, kb + tid, a.P, a.L);
   };
-  auto store_step = [&](bf16_t *dK, bf16_t *dV, int *dW) {
-    if constexpr (kDirect) {
-      __builtin_amdgcn_s_waitcnt(0);   // this thread's direct loads have landed
-    } else {
-      stK.store(dK);
-      stV.store(dV);
-    }
+  auto store_step = [&](bf16_t *, bf16_t *, int *dW) {
+    __builtin_amdgcn_s_waitcnt(0);   // this thread's direct loads have landed
     if (tid < kStepKeys) *reinterpret_cast<int *>(const_cast<char *>(lds_at(dW, opaque_u32(tid * 4u)))) = wkey.w();
   };
 
@@ -327,8 +312,6 @@ template __global__ void attn_fwd_kernel<1, 128, bf16_t>(AttnArgs);
 template __global__ void attn_fwd_kernel<1, 64, bf16_t>(AttnArgs);
 template __global__ void attn_fwd_kernel<1, 128, f16_t>(AttnArgs);
 template __global__ void attn_fwd_kernel<1, 64, f16_t>(AttnArgs);
-template __global__ void attn_fwd_kernel<1, 128, float>(AttnArgs);
-template __global__ void attn_fwd_kernel<1, 64, float>(AttnArgs);
 
 // NB = 1 (32 rows per wave, 2 waves per SIMD): measured 1.01 ms against
 // 1.66 ms for NB = 2 at Qwen3-8B geometry (4096 + 1024 rows vs an 8192 prefix).
@@ -345,13 +328,13 @@ static void fwd_launch(const AttnArgs &a, hipStream_t st) {
 
 template <int HD>
 static void fwd_launch_dt(const AttnArgs &a, int dtype, hipStream_t st) {
-  if (dtype == kDtF32) fwd_launch<HD, float>(a, st);
-  else if (dtype == kDtF16) fwd_launch<HD, f16_t>(a, st);
+  if (dtype == kDtF16) fwd_launch<HD, f16_t>(a, st);
   else fwd_launch<HD, bf16_t>(a, st);
 }
 
 void launch_attn_fwd(const AttnArgs &a, int head_dim, int dtype, hipStream_t st) {
-  if (head_dim == 128) fwd_launch_dt<128>(a, dtype, st);
+  if (dtype == kDtF32) launch_attn_fwd_f32(a, head_dim, st);
+  else if (head_dim == 128) fwd_launch_dt<128>(a, dtype, st);
   else fwd_launch_dt<64>(a, dtype, st);
 }
 

@@ -50,6 +50,9 @@ void launch_attn_fwd(const AttnArgs &a, int head_dim, int dtype, hipStream_t str
 constexpr int kBwdDq = 1;
 constexpr int kBwdDkDv = 2;
 void launch_attn_bwd(const AttnArgs &a, int head_dim, int dtype, int passes, hipStream_t stream);
+// fp32 operands (mga_attn_f32.hip): fp32 MFMAs throughout; same contract.
+void launch_attn_fwd_f32(const AttnArgs &a, int head_dim, hipStream_t stream);
+void launch_attn_bwd_f32(const AttnArgs &a, int head_dim, int passes, hipStream_t stream);
 
 // Fused Qwen3 q/k RMSNorm + rotary embedding (mga_qk_rope.hip). Operands are
 // [S, heads, D] addressed with (token stride, head stride) in elements; cos

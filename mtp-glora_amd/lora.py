@@ -22,8 +22,10 @@ and gate are applied to the rank-r activations before lora_B rather than to
 lora_B's output (the same value when the scaling is a power of two and the
 gate is 0 / 1, as in the reference's configurations), and the base product
 is accumulated in fp32 onto the rounded LoRA term before one final rounding
-(in the backward likewise for dX). bf16 only,
-no biases (Qwen3 and Llama projections have none), base weights frozen.
+(in the backward likewise for dX). bf16 only: GatedLoRALinear and
+apply_lora_to_model raise TypeError for a base layer of another dtype (before
+apply_lora_to_model changes anything); no biases (Qwen3 and Llama
+projections have none), base weights frozen.
 """
 from __future__ import annotations
 
@@ -155,6 +157,7 @@ class GatedLoRALinear(nn.Module):
     def __init__(self, base_layer: nn.Linear, rank: int, alpha: float, dropout: float, lora_bias: bool,
                  use_rslora: bool):
         super().__init__()
+        _check_base_dtype("base_layer", base_layer)
         self.base_layer = base_layer
         self.rank = rank
         self.alpha = alpha
@@ -176,6 +179,12 @@ class GatedLoRALinear(nn.Module):
                                  self.lora_scaling, p)
 
 
+def _check_base_dtype(name: str, layer: nn.Linear) -> None:
+    if layer.weight.dtype != torch.bfloat16:
+        raise TypeError(f"{name}: the fused gated LoRA layer supports bfloat16 base layers only "
+                        f"(got {layer.weight.dtype}); convert the model with .to(torch.bfloat16) first")
+
+
 def _freeze_base_and_enable_lora(model: nn.Module) -> None:
     for name, param in model.named_parameters():
         param.requires_grad = "lora_" in name
@@ -187,15 +196,18 @@ def apply_lora_to_model(model: nn.Module, target_modules: List[str] = None, rank
     ``GatedLoRALinear`` (the reference's rule, gated_lora.py:61-100)."""
     targets = target_modules or ["qkv_proj", "o_proj", "gate_up_proj", "down_proj"]
 
-    def visit(module: nn.Module):
+    def matches(module: nn.Module, prefix: str = ""):
         for name, child in module.named_children():
             if isinstance(child, nn.Linear):
                 if any(t in name for t in targets):
-                    mult = 3 if "qkv_proj" in name else (2 if "gate_up_proj" in name else 1)
-                    setattr(module, name, GatedLoRALinear(child, mult * rank, mult * alpha, dropout, lora_bias,
-                                                          use_rslora))
+                    yield module, name, child, prefix + name
             else:
-                visit(child)
+                yield from matches(child, prefix + name + ".")
 
-    visit(model)
+    found = list(matches(model))
+    for _, _, child, path in found:   # every target checked before the model changes
+        _check_base_dtype(path, child)
+    for module, name, child, _ in found:
+        mult = 3 if "qkv_proj" in name else (2 if "gate_up_proj" in name else 1)
+        setattr(module, name, GatedLoRALinear(child, mult * rank, mult * alpha, dropout, lora_bias, use_rslora))
     _freeze_base_and_enable_lora(model)

@@ -6,7 +6,8 @@ bit-exact. fp16 operands (three more mantissa bits than bf16, so every
 rounding the kernels share with the reference's flex path -- the
 probabilities and dS before their products, the outputs -- is 8x smaller):
 max-abs <= 4e-3, mean-abs <= 4e-4, gradients with the max bound relative
-above magnitude 1."""
+above magnitude 1. fp32 operands (fp32 MFMAs, no 16-bit rounding anywhere):
+max-abs <= 1e-5, mean-abs <= 1e-6, relative above magnitude 1."""
 import numpy as np
 import pytest
 import torch
@@ -45,26 +46,30 @@ def run_case(mga, dev, n_reg, n_anchor, draft, P, Hq, Hkv, D, dtype=torch.bfloat
 
 F16_MAX_ABS = 4e-3
 F16_MEAN_ABS = 4e-4
+F32_MAX_ABS = 1e-5
+F32_MEAN_ABS = 1e-6
 
 
 def compare_oracle(seq, P, q, k, v, kp, vp, do, o, lse, D, grad_start, max_abs=MAX_ABS, mean_abs=MEAN_ABS,
-                   grad_scaled=False):
+                   scaled=False, tensor_scale=False):
+    """scaled: max bounds relative above magnitude 1; tensor_scale: bounds
+    times max(1, max |ref|) of each tensor (gpu_helpers.check)."""
     allowed = mo.mtp_mask_dense(seq.gate, P)
     qn = f64(q)[0]
     kn = np.concatenate([f64(kp)[0], f64(k)[0]], axis=1)
     vn = np.concatenate([f64(vp)[0], f64(v)[0]], axis=1)
     on, lsen = mo.attention_fwd(qn, kn, vn, allowed, D ** -0.5)
-    tol = dict(max_abs=max_abs, mean_abs=mean_abs)
-    check("o", f64(o)[0].transpose(1, 0, 2), on, **tol)
+    tol = dict(max_abs=max_abs, mean_abs=mean_abs, tensor_scale=tensor_scale)
+    check("o", f64(o)[0].transpose(1, 0, 2), on, **tol, scale_above_one=scaled)
     got_lse = f64(lse)[0]
     assert np.array_equal(np.isneginf(got_lse), np.isneginf(lsen))
     fin = np.isfinite(lsen)
-    check("lse", got_lse[fin], lsen[fin], **tol, scale_above_one=grad_scaled)
+    check("lse", got_lse[fin], lsen[fin], **tol, scale_above_one=scaled)
     dqn, dkn, dvn = mo.attention_bwd(qn, kn, vn, on, lsen, f64(do)[0].transpose(1, 0, 2),
                                      allowed, D ** -0.5, grad_start=grad_start)
-    check("dq", f64(q.grad)[0], dqn, **tol, scale_above_one=grad_scaled)
-    check("dk", f64(k.grad)[0], dkn[:, -k.shape[2]:], **tol, scale_above_one=grad_scaled)
-    check("dv", f64(v.grad)[0], dvn[:, -v.shape[2]:], **tol, scale_above_one=grad_scaled)
+    check("dq", f64(q.grad)[0], dqn, **tol, scale_above_one=scaled)
+    check("dk", f64(k.grad)[0], dkn[:, -k.shape[2]:], **tol, scale_above_one=scaled)
+    check("dv", f64(v.grad)[0], dvn[:, -v.shape[2]:], **tol, scale_above_one=scaled)
 
 
 SMALL = [
@@ -94,7 +99,7 @@ def test_attention_small_fp16(mga, dev, c):
     seq, q, k, v, kp, vp, do, o, lse = run_case(mga, dev, dtype=torch.float16, seed=3, **c)
     assert o.dtype == torch.float16 and q.grad.dtype == torch.float16 and k.grad.dtype == torch.float16
     compare_oracle(seq, c["P"], q, k, v, kp, vp, do, o, lse, c["D"], grad_start=c["P"],
-                   max_abs=F16_MAX_ABS, mean_abs=F16_MEAN_ABS, grad_scaled=True)
+                   max_abs=F16_MAX_ABS, mean_abs=F16_MEAN_ABS, scaled=True)
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
@@ -136,12 +141,27 @@ def test_attention_large_logits(mga, dev, dtype):
         check(name, f64(got)[0], ref, max_abs=3 * mx, mean_abs=3 * mn)
 
 
-@pytest.mark.parametrize("D", [64, 128])
-def test_attention_fp32_operands(mga, dev, D):
-    c = dict(n_reg=256, n_anchor=16, draft=4, P=128, Hq=4, Hkv=2, D=D)
-    seq, q, k, v, kp, vp, do, o, lse = run_case(mga, dev, dtype=torch.float32, **c)
-    assert o.dtype == torch.float32 and q.grad.dtype == torch.float32
-    compare_oracle(seq, c["P"], q, k, v, kp, vp, do, o, lse, D, grad_start=c["P"])
+@pytest.mark.parametrize("c", SMALL)
+def test_attention_small_fp32(mga, dev, c):
+    """fp32 operands run the fp32 MFMAs: fp32 products, softmax and
+    gradients, as the reference computes an fp32 model's attention."""
+    seq, q, k, v, kp, vp, do, o, lse = run_case(mga, dev, dtype=torch.float32, seed=5, **c)
+    assert o.dtype == torch.float32 and q.grad.dtype == torch.float32 and k.grad.dtype == torch.float32
+    compare_oracle(seq, c["P"], q, k, v, kp, vp, do, o, lse, c["D"], grad_start=c["P"],
+                   max_abs=F32_MAX_ABS, mean_abs=F32_MEAN_ABS, scaled=True)
+
+
+def test_attention_large_logits_fp32(mga, dev):
+    """The large-logit case of the 16-bit test in fp32: no 16-bit rounding,
+    so the fp32 bounds hold, scaled by each tensor's largest magnitude (the
+    raw scores reach about 45 here, where fp32 spacing is 4e-6, so every
+    probability carries a relative error near 1e-6; an output summed from
+    terms of magnitude 8 -- v ~ N(0, 2^2) -- then has an absolute error near
+    1e-5 whatever its own size)."""
+    c = dict(n_reg=320, n_anchor=24, draft=4, P=192, Hq=4, Hkv=2, D=128)
+    seq, q, k, v, kp, vp, do, o, lse = run_case(mga, dev, dtype=torch.float32, seed=11, std=2.0, **c)
+    compare_oracle(seq, c["P"], q, k, v, kp, vp, do, o, lse, c["D"], grad_start=c["P"],
+                   max_abs=F32_MAX_ABS, mean_abs=F32_MEAN_ABS, tensor_scale=True)
 
 
 def test_plain_key_tensor_gets_full_gradient(mga, dev):
@@ -197,6 +217,13 @@ def test_attention_full_config_fp16(mga, dev):
     """Config 2's geometry with fp16 operands, fp16 bounds."""
     full_config_case(mga, dev, dict(n_reg=4096, n_anchor=256, draft=4, P=8192), torch.float16,
                      max_abs=F16_MAX_ABS, mean_abs=F16_MEAN_ABS, grad_scaled=True)
+
+
+def test_attention_full_config_fp32(mga, dev):
+    """Config 2's geometry with fp32 operands against the fp32 dense
+    reference (its own fp32 rounding included in the bound)."""
+    full_config_case(mga, dev, dict(n_reg=4096, n_anchor=256, draft=4, P=8192), torch.float32,
+                     max_abs=F32_MAX_ABS, mean_abs=F32_MEAN_ABS, grad_scaled=True)
 
 
 def full_config_case(mga, dev, cfg, dtype, max_abs=MAX_ABS, mean_abs=MEAN_ABS, grad_scaled=False):

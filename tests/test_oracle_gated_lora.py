@@ -117,7 +117,7 @@ def test_keep_mask_properties():
 
 def test_module_mirror_construction():
     mod = importlib.import_module("mtp-glora_amd")
-    base = torch.nn.Linear(64, 48, bias=False)
+    base = torch.nn.Linear(64, 48, bias=False, dtype=torch.bfloat16)
     layer = mod.GatedLoRALinear(base, rank=8, alpha=16, dropout=0.05, lora_bias=False, use_rslora=False)
     assert layer.lora_scaling == 2.0 and layer.rank == 8 and layer.alpha == 16
     assert isinstance(layer.dropout, torch.nn.Dropout) and layer.dropout.p == 0.05
@@ -126,10 +126,10 @@ def test_module_mirror_construction():
     assert layer.lora_B.weight.abs().max().item() == 0.0 and layer.lora_A.weight.abs().max().item() > 0
     rs = mod.GatedLoRALinear(base, rank=16, alpha=32, dropout=0.0, lora_bias=False, use_rslora=True)
     assert rs.lora_scaling == pytest.approx(32 / 4) and isinstance(rs.dropout, torch.nn.Identity)
+    assert layer.lora_A.weight.dtype == torch.bfloat16
 
 
-def test_apply_lora_to_model_wraps_and_freezes():
-    mod = importlib.import_module("mtp-glora_amd")
+def _lora_net(dtype):
 
     class Attn(torch.nn.Module):
         def __init__(self):
@@ -149,7 +149,12 @@ def test_apply_lora_to_model_wraps_and_freezes():
             self.attn, self.mlp = Attn(), Mlp()
             self.lm_head = torch.nn.Linear(32, 100, bias=False)
 
-    net = Net()
+    return Net().to(dtype)
+
+
+def test_apply_lora_to_model_wraps_and_freezes():
+    mod = importlib.import_module("mtp-glora_amd")
+    net = _lora_net(torch.bfloat16)
     mod.apply_lora_to_model(net, rank=4, alpha=8, dropout=0.0)
     assert isinstance(net.attn.qkv_proj, mod.GatedLoRALinear) and net.attn.qkv_proj.rank == 12
     assert net.attn.qkv_proj.alpha == 24 and net.attn.qkv_proj.lora_scaling == 2.0
@@ -158,3 +163,18 @@ def test_apply_lora_to_model_wraps_and_freezes():
     trainable = sorted(n for n, p in net.named_parameters() if p.requires_grad)
     assert trainable and all("lora_" in n for n in trainable)
     assert not net.attn.qkv_proj.base_layer.weight.requires_grad
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_apply_lora_to_model_refuses_other_dtypes_up_front(dtype):
+    """The fused layer is bf16 only: a model of another dtype gets a TypeError
+    naming the first target layer, before any layer is wrapped or frozen."""
+    mod = importlib.import_module("mtp-glora_amd")
+    net = _lora_net(dtype)
+    net.mlp.down_proj.to(torch.bfloat16)   # one matching layer of the right dtype changes nothing
+    with pytest.raises(TypeError, match="attn.qkv_proj.*bfloat16"):
+        mod.apply_lora_to_model(net, rank=4, alpha=8, dropout=0.0)
+    assert not any(isinstance(m, mod.GatedLoRALinear) for m in net.modules())
+    assert all(p.requires_grad for p in net.parameters())
+    with pytest.raises(TypeError, match="bfloat16"):
+        mod.GatedLoRALinear(torch.nn.Linear(8, 8, bias=False, dtype=dtype), 4, 8, 0.0, False, False)
