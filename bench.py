@@ -206,6 +206,33 @@ def qk_rope_phase(torch, timer, S: int, Hq: int, Hkv: int, D: int, n: int, cpu_t
         torch.autograd.backward([eq, ek], [go_q.transpose(1, 2), go_k.transpose(1, 2)])
 
     t_eager = timer(lambda: eager_step(q, k, cos, sin, qw, kw, gq, gk), n)
+
+    # the chunk's keys and values into the KV cache rows [P, P + S) of a
+    # layer: norm / RoPE, then the cache update's copy of K and V, against the
+    # one launch that writes the post-RoPE keys and the values into the rows
+    ops = import_module("mtp-glora_amd.ops")
+    v = torch.randn(1, S, Hkv, D, generator=g, device=dev).to(bf)
+    Pc = 8192
+    kbuf = torch.empty(Hkv, Pc + S, D, device=dev, dtype=bf)
+    vbuf = torch.empty(Hkv, Pc + S, D, device=dev, dtype=bf)
+
+    def copy_path():
+        _, ko, _ = rope.norm_rope_forward(q, k, qw, kw, cos, sin, 1e-6)
+        ops.kv_append(ko.transpose(1, 2), v.transpose(1, 2), kbuf, vbuf, dst_offset=Pc)
+
+    def fused_path():
+        rope.norm_rope_stage_forward(q, k, v, qw, kw, cos, sin, 1e-6, kbuf[None, :, Pc:], vbuf[None, :, Pc:])
+
+    t_copy = graph_time(torch, copy_path, 20)
+    t_fused = graph_time(torch, fused_path, 20)
+    kv_rows = S * Hkv * D * 2
+    stage = {"prefix": Pc, "copy_path_ms": round(t_copy, 5), "fused_ms": round(t_fused, 5),
+             "bytes_copy_path": fwd_bytes + 4 * kv_rows, "bytes_fused": fwd_bytes + 2 * kv_rows,
+             "launches_copy_path": 2, "launches_fused": 1,
+             "what": "norm/RoPE of q and k with the chunk's K and V staged into the cache rows [P, P+S): "
+                     "norm_rope_forward + kv_append (post-RoPE K written, read back and written again, V "
+                     "read and written) against mga_qk_norm_rope_stage_fwd (K written once into the rows, "
+                     "V copied in the same launch)"}
     args_cpu = [t_[:, :cpu_tokens].cpu() if t_.dim() == 4 else t_.cpu() for t_ in (q, k)]
     c_cpu, s_cpu = cos[:, :cpu_tokens].cpu(), sin[:, :cpu_tokens].cpu()
     secs = []
@@ -220,7 +247,7 @@ def qk_rope_phase(torch, timer, S: int, Hq: int, Hkv: int, D: int, n: int, cpu_t
             "fwd_GBps": round(fwd_gbps, 1), "bwd_GBps": round(bwd_gbps, 1),
             "fwd_frac": round(fwd_gbps / PEAK_HBM_GBPS, 4), "bwd_frac": round(bwd_gbps / PEAK_HBM_GBPS, 4),
             "peak": PEAK_HBM_GBPS, "bytes": {"fwd": fwd_bytes, "bwd": bwd_bytes},
-            "fwd_ms_eager_launches": round(t_f_eager, 5),
+            "fwd_ms_eager_launches": round(t_f_eager, 5), "cache_stage": stage,
             "torch_eager_gpu_fwd_bwd_ms": round(t_eager, 4),
             "cpu_tokens_per_s": round(cpu_tokens / cpu_s, 1),
             "gpu_tokens_per_s": round(S / ((t_f + t_b) * 1e-3), 1),

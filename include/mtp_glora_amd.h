@@ -217,6 +217,33 @@ int mga_qk_norm_rope_fwd(const void *q, int64_t q_token_stride, int64_t q_head_s
                          float *rstd, void *stream);
 
 /*
+ * mga_qk_norm_rope_fwd that also copies the value rows v [S, Hkv, D] to
+ * v_out unchanged, in the same launch: with k_out / v_out pointing at a
+ * layer's KV-cache rows [P, P + S) (for a [Hkv, capacity, D] cache buffer:
+ * base + P * D, token stride D, head stride capacity * D) it writes the
+ * chunk's post-RoPE keys and its values where the cache update
+ * (DynamicLayer.update via Cache.update, [tf]cache_utils.py:1349-1381, called
+ * at modeling_qwen3.py:281-284) would copy them, so no separate append runs.
+ *   - q may be null (with q_weight, q_out and rstd ignored / null): keys and
+ *     values only, e.g. to re-stage a chunk's regular rows into the prefix;
+ *   - rows may be null; else output row s (s < S) reads input row rows[s] of
+ *     q / k / v and cos / sin row rows[s], and rows outside [0, src_rows) are
+ *     skipped (the regular-token gather of collator.py:270-277);
+ *   - rstd may be null (nothing saved for a backward).
+ */
+int mga_qk_norm_rope_stage_fwd(const void *q, int64_t q_token_stride, int64_t q_head_stride,
+                               const void *k, int64_t k_token_stride, int64_t k_head_stride,
+                               const void *v, int64_t v_token_stride, int64_t v_head_stride,
+                               const void *q_weight, const void *k_weight,
+                               const void *cos, const void *sin, int64_t cs_stride, float eps,
+                               const int32_t *rows, int32_t src_rows,
+                               int32_t S, int32_t Hq, int32_t Hkv, int32_t head_dim, int32_t dtype,
+                               void *q_out, int64_t qo_token_stride, int64_t qo_head_stride,
+                               void *k_out, int64_t ko_token_stride, int64_t ko_head_stride,
+                               void *v_out, int64_t vo_token_stride, int64_t vo_head_stride,
+                               float *rstd, void *stream);
+
+/*
  * Backward of mga_qk_norm_rope_fwd for q and k (the norm weights, cos and sin
  * get no gradient): given the output gradients dq_out / dk_out, writes
  *   dx = r * dy - (r^3 / D) * x * sum(dy * x),  dy = w * dn,

@@ -53,6 +53,9 @@ SIGNATURES = {
                              _I32, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _I32, _P],
     "mga_qk_norm_rope_fwd": [_P, _I64, _I64, _P, _I64, _I64, _P, _P, _P, _P, _I64, _F32,
                              _I32, _I32, _I32, _I32, _I32, _P, _I64, _I64, _P, _I64, _I64, _P, _P],
+    "mga_qk_norm_rope_stage_fwd": [_P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _P, _P, _P, _I64, _F32,
+                                   _P, _I32, _I32, _I32, _I32, _I32, _I32, _P, _I64, _I64, _P, _I64, _I64,
+                                   _P, _I64, _I64, _P, _P],
     "mga_qk_norm_rope_bwd": [_P, _I64, _I64, _P, _I64, _I64, _P, _P, _P, _P, _I64, _P,
                              _I32, _I32, _I32, _I32, _I32, _P, _I64, _I64, _P, _I64, _I64,
                              _P, _I64, _I64, _P, _I64, _I64, _P],

@@ -107,21 +107,47 @@ class StreamingKVCache:
         torch.autograd.graph.increment_version(self._k[layer_idx])
         torch.autograd.graph.increment_version(self._v[layer_idx])
 
+    def stage_rows(self, layer_idx: int, like: torch.Tensor):
+        """``[1, Hkv, S, D]`` views of rows ``[P, P + S)`` of the layer's K and V
+        buffers (S and the dims from ``like``), for a kernel that writes the
+        chunk's K/V there itself; ``update`` given these views copies nothing."""
+        self._ensure(layer_idx, like)
+        P, S = self.prefix_len, like.shape[2]
+        if P + S > self.capacity:
+            raise RuntimeError(f"StreamingKVCache capacity {self.capacity} exceeded ({P} + {S} rows)")
+        return self._k[layer_idx][None, :, P:P + S], self._v[layer_idx][None, :, P:P + S]
+
+    @staticmethod
+    def _in_place(t: torch.Tensor, buf: torch.Tensor, P: int) -> bool:
+        return (t.data_ptr() == buf[:, P].data_ptr() and t.stride()[1:] == buf.stride()
+                and t.shape[1] == buf.shape[0])
+
     # -- Cache API ------------------------------------------------------------
     def update(self, key_states: torch.Tensor, value_states: torch.Tensor, layer_idx: int,
                cache_kwargs=None):
         """Stage the chunk's K/V after the cached prefix and return the full
-        ``[1, Hkv, P + S, D]`` K and V."""
+        ``[1, Hkv, P + S, D]`` K and V. K/V that already are the views of
+        ``stage_rows`` are not copied."""
         self._ensure(layer_idx, key_states)
         if value_states.shape != key_states.shape:
             raise ValueError("key and value states must have the same shape")
         P = self.prefix_len
         S = key_states.shape[2]
         kb, vb = self._k[layer_idx], self._v[layer_idx]
-        ops.kv_append(key_states, value_states, kb, vb, dst_offset=P)   # raises on capacity
+        in_place = self._in_place(key_states, kb, P), self._in_place(value_states, vb, P)
+        if in_place == (True, True):
+            restage = getattr(key_states, "_mga_restage", None)
+            if restage is None:
+                raise ValueError("key / value states sit in the cache rows without a way to re-stage their "
+                                 "regular rows (stage them with rope.qk_norm_rope_stage)")
+            self._staged[layer_idx] = restage
+        elif any(in_place):
+            raise ValueError("only one of key / value states sits in the cache rows")
+        else:
+            ops.kv_append(key_states, value_states, kb, vb, dst_offset=P)   # raises on capacity
+            self._staged[layer_idx] = (key_states, value_states)
         self._bump(layer_idx)
         self._len[layer_idx] = P + S
-        self._staged[layer_idx] = (key_states, value_states)
         kf = kb[None, :, :P + S]
         vf = vb[None, :, :P + S]
         if key_states.requires_grad:
@@ -178,9 +204,12 @@ class StreamingKVCache:
             st = self._staged[layer]
             if st is None:
                 raise RuntimeError(f"layer {layer} has no staged chunk to commit")
-            k_cur, v_cur = st
-            ops.kv_append(k_cur.detach(), v_cur.detach(), self._k[layer], self._v[layer],
-                          dst_offset=P, idx=idx, n_rows=n_regular)
+            if callable(st):   # staged in place: re-staged from the projections
+                st(idx, n_regular, self._k[layer], self._v[layer], P)
+            else:
+                k_cur, v_cur = st
+                ops.kv_append(k_cur.detach(), v_cur.detach(), self._k[layer], self._v[layer],
+                              dst_offset=P, idx=idx, n_rows=n_regular)
             self._bump(layer)
         self.prefix_len = P + n_regular
         self._len = [self.prefix_len] * self.num_layers

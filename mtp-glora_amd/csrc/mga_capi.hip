@@ -283,6 +283,39 @@ int check_qk_rope(const char *fn, const void *q, const void *k, const void *qw, 
 
 }  // namespace
 
+namespace {
+
+int qk_rope_fwd(const char *fn, const void *q, int64_t q_ss, int64_t q_hs, const void *k, int64_t k_ss,
+                int64_t k_hs, const void *v, int64_t v_ss, int64_t v_hs, const void *q_weight, const void *k_weight,
+                const void *cos, const void *sin, int64_t cs_ss, float eps, const int32_t *rows, int32_t src_rows,
+                int32_t S, int32_t Hq, int32_t Hkv, int32_t head_dim, int32_t dtype, void *q_out, int64_t qo_ss,
+                int64_t qo_hs, void *k_out, int64_t ko_ss, int64_t ko_hs, void *v_out, int64_t vo_ss,
+                int64_t vo_hs, float *rstd, void *stream) {
+  if (!elem_bytes(dtype)) return fail(MGA_ERR_INVALID, "%s: unknown dtype code %d", fn, dtype);
+  if (S <= 0 || Hkv <= 0 || (q && Hq <= 0)) return fail(MGA_ERR_INVALID, "%s: bad sizes (S=%d Hq=%d Hkv=%d)", fn, S, Hq, Hkv);
+  if (head_dim <= 0 || head_dim > 128 || (head_dim & 1))
+    return fail(MGA_ERR_INVALID, "%s: head_dim must be even and <= 128 (got %d)", fn, head_dim);
+  if (!k || !k_weight || !cos || !sin || !k_out) return fail(MGA_ERR_INVALID, "%s: null pointer argument", fn);
+  if (q && (!q_weight || !q_out)) return fail(MGA_ERR_INVALID, "%s: query without its weight or output", fn);
+  if (!q && (q_out || rstd)) return fail(MGA_ERR_INVALID, "%s: query output or rstd without a query", fn);
+  if ((v == nullptr) != (v_out == nullptr)) return fail(MGA_ERR_INVALID, "%s: value operand without its output", fn);
+  if (rows && src_rows <= 0) return fail(MGA_ERR_INVALID, "%s: row gather needs src_rows > 0 (got %d)", fn, src_rows);
+  mga::QkRopeArgs a = {};
+  a.q = q; a.q_ss = q_ss; a.q_hs = q_hs;
+  a.k = k; a.k_ss = k_ss; a.k_hs = k_hs;
+  a.v = v; a.v_ss = v_ss; a.v_hs = v_hs;
+  a.qw = q_weight; a.kw = k_weight; a.cos = cos; a.sin = sin; a.cs_ss = cs_ss;
+  a.qo = q_out; a.qo_ss = qo_ss; a.qo_hs = qo_hs;
+  a.ko = k_out; a.ko_ss = ko_ss; a.ko_hs = ko_hs;
+  a.vo = v_out; a.vo_ss = vo_ss; a.vo_hs = vo_hs;
+  a.rows = rows; a.src_rows = src_rows;
+  a.rstd = rstd; a.eps = eps; a.S = S; a.Hq = q ? Hq : 0; a.Hkv = Hkv; a.D = head_dim;
+  mga::launch_qk_norm_rope(a, dtype, false, (hipStream_t)stream);
+  return check_launch(fn);
+}
+
+}  // namespace
+
 int mga_qk_norm_rope_fwd(const void *q, int64_t q_ss, int64_t q_hs, const void *k, int64_t k_ss, int64_t k_hs,
                          const void *q_weight, const void *k_weight, const void *cos, const void *sin,
                          int64_t cs_ss, float eps, int32_t S, int32_t Hq, int32_t Hkv, int32_t head_dim,
@@ -290,16 +323,22 @@ int mga_qk_norm_rope_fwd(const void *q, int64_t q_ss, int64_t q_hs, const void *
                          int64_t ko_hs, float *rstd, void *stream) {
   int rc = check_qk_rope("mga_qk_norm_rope_fwd", q, k, q_weight, k_weight, cos, sin, rstd, S, Hq, Hkv, head_dim, dtype);
   if (rc != MGA_OK) return rc;
-  if (!q_out || !k_out) return fail(MGA_ERR_INVALID, "mga_qk_norm_rope_fwd: null output");
-  mga::QkRopeArgs a = {};
-  a.q = q; a.q_ss = q_ss; a.q_hs = q_hs;
-  a.k = k; a.k_ss = k_ss; a.k_hs = k_hs;
-  a.qw = q_weight; a.kw = k_weight; a.cos = cos; a.sin = sin; a.cs_ss = cs_ss;
-  a.qo = q_out; a.qo_ss = qo_ss; a.qo_hs = qo_hs;
-  a.ko = k_out; a.ko_ss = ko_ss; a.ko_hs = ko_hs;
-  a.rstd = rstd; a.eps = eps; a.S = S; a.Hq = Hq; a.Hkv = Hkv; a.D = head_dim;
-  mga::launch_qk_norm_rope(a, dtype, false, (hipStream_t)stream);
-  return check_launch("mga_qk_norm_rope_fwd");
+  return qk_rope_fwd("mga_qk_norm_rope_fwd", q, q_ss, q_hs, k, k_ss, k_hs, nullptr, 0, 0, q_weight, k_weight, cos,
+                     sin, cs_ss, eps, nullptr, 0, S, Hq, Hkv, head_dim, dtype, q_out, qo_ss, qo_hs, k_out, ko_ss,
+                     ko_hs, nullptr, 0, 0, rstd, stream);
+}
+
+int mga_qk_norm_rope_stage_fwd(const void *q, int64_t q_ss, int64_t q_hs, const void *k, int64_t k_ss,
+                               int64_t k_hs, const void *v, int64_t v_ss, int64_t v_hs, const void *q_weight,
+                               const void *k_weight, const void *cos, const void *sin, int64_t cs_ss, float eps,
+                               const int32_t *rows, int32_t src_rows, int32_t S, int32_t Hq, int32_t Hkv,
+                               int32_t head_dim, int32_t dtype, void *q_out, int64_t qo_ss, int64_t qo_hs,
+                               void *k_out, int64_t ko_ss, int64_t ko_hs, void *v_out, int64_t vo_ss,
+                               int64_t vo_hs, float *rstd, void *stream) {
+  if (!v || !v_out) return fail(MGA_ERR_INVALID, "mga_qk_norm_rope_stage_fwd: null value operand");
+  return qk_rope_fwd("mga_qk_norm_rope_stage_fwd", q, q_ss, q_hs, k, k_ss, k_hs, v, v_ss, v_hs, q_weight, k_weight,
+                     cos, sin, cs_ss, eps, rows, src_rows, S, Hq, Hkv, head_dim, dtype, q_out, qo_ss, qo_hs, k_out,
+                     ko_ss, ko_hs, v_out, vo_ss, vo_hs, rstd, stream);
 }
 
 int mga_qk_norm_rope_bwd(const void *q, int64_t q_ss, int64_t q_hs, const void *k, int64_t k_ss, int64_t k_hs,

@@ -63,13 +63,17 @@ struct QkRopeArgs {
   const void *qw, *kw, *cos, *sin; int64_t cs_ss;
   void *qo; int64_t qo_ss, qo_hs;     // forward outputs
   void *ko; int64_t ko_ss, ko_hs;
+  const void *v; int64_t v_ss, v_hs;  // forward, optional: value rows copied to vo unchanged
+  void *vo; int64_t vo_ss, vo_hs;
+  const int32_t *rows;                // forward, optional: output row s reads input row rows[s]
+  int32_t src_rows;                   //   (and cos / sin row rows[s]); rows outside [0, src_rows) are skipped
   const void *dqo; int64_t dqo_ss, dqo_hs;   // backward: gradients of the outputs
   const void *dko; int64_t dko_ss, dko_hs;
   void *dq; int64_t dq_ss, dq_hs;     // backward outputs
   void *dk; int64_t dk_ss, dk_hs;
-  float *rstd;
+  float *rstd;                        // forward: may be null (nothing saved)
   float eps;
-  int32_t S, Hq, Hkv, D;
+  int32_t S, Hq, Hkv, D;              // forward with q null: key (and value) rows only
 };
 void launch_qk_norm_rope(const QkRopeArgs &a, int dtype, bool backward, hipStream_t stream);
 

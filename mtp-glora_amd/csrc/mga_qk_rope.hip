@@ -11,6 +11,9 @@
 //   rotate_half(n) = [-n[D/2:], n[:D/2]],
 // T rounding to the model dtype after each op as the reference's torch ops do
 // (fp contraction is off in the forward so fp32 models round each op too).
+// The forward can also copy the value rows, so one launch writes a layer's
+// post-RoPE keys and its values straight into their KV-cache rows (the
+// cache update of modeling_qwen3.py:281-284 then has nothing left to copy).
 //
 // Layout: grid (token, head block), one wave per workgroup. A group of G lanes
 // (a power of two, G * V >= D / 2) owns one (token, head) row; a wave's 64 / G
@@ -143,11 +146,13 @@ __device__ __forceinline__ float group_sum(float v, int lg) {
 }  // namespace
 
 // The rows one wave works on: block blockIdx.y of the token's query heads
-// (blocks 0 .. nbq - 1) or key heads (the rest), one head per lane group.
+// (blocks 0 .. nbq - 1), key heads (the next nbk) or, in a forward that
+// stages the values too, value heads (the last nbk), one head per lane group.
 // Everything here is wave-uniform.
 template <typename T>
 struct Block {
   bool isq;
+  bool isv;          // a value row copy, no normalisation
   int h0;            // first head of the block
   int nh;            // heads of this operand
   int rstd0;         // rstd index of head 0 of this operand within the token
@@ -155,11 +160,12 @@ struct Block {
 
 template <typename T>
 __device__ __forceinline__ Block<T> block_of(const QkRopeArgs &a, int ngrp) {
-  const int nbq = (a.Hq + ngrp - 1) / ngrp;
+  const int nbq = a.q ? (a.Hq + ngrp - 1) / ngrp : 0, nbk = (a.Hkv + ngrp - 1) / ngrp;
   const int b = blockIdx.y;
   Block<T> k;
   k.isq = b < nbq;
-  k.h0 = (k.isq ? b : b - nbq) * ngrp;
+  k.isv = b >= nbq + nbk;   // the forward's value-copy blocks (a.v set)
+  k.h0 = (k.isq ? b : (k.isv ? b - nbq - nbk : b - nbq)) * ngrp;
   k.nh = k.isq ? a.Hq : a.Hkv;
   k.rstd0 = k.isq ? 0 : a.Hq;
   return k;
@@ -170,15 +176,23 @@ __device__ __forceinline__ Block<T> block_of(const QkRopeArgs &a, int ngrp) {
 template <typename T, int V>
 __global__ __launch_bounds__(64) void qk_norm_rope_fwd_kernel(QkRopeArgs a, int lg, float inv_d) {
 #pragma clang fp contract(off)
-  const int s = blockIdx.x;
+  const int so = blockIdx.x;   // output row
   const int lane = threadIdx.x;
   const int j = lane & ((1 << lg) - 1), ngrp = 64 >> lg;
   const Block<T> b = block_of<T>(a, ngrp);
   const int h = b.h0 + (lane >> lg);
   if (h >= b.nh) return;   // whole groups leave together
+  const int s = a.rows ? a.rows[so] : so;   // input row (and cos / sin row)
+  if (a.rows && (s < 0 || s >= a.src_rows)) return;
   const int half = a.D >> 1;
   const bool on = j * V < half;
   const int d = on ? j * V : 0;
+  if (b.isv) {   // stage the value row (e.g. into its cache row), unchanged
+    Half2<T, V> v;
+    v.load(reinterpret_cast<const T *>(a.v) + (int64_t)s * a.v_ss + (int64_t)h * a.v_hs + d, half);
+    if (on) v.store(reinterpret_cast<T *>(a.vo) + (int64_t)so * a.vo_ss + (int64_t)h * a.vo_hs + d, half);
+    return;
+  }
   const T *x0 = reinterpret_cast<const T *>(b.isq ? a.q : a.k) + (int64_t)s * (b.isq ? a.q_ss : a.k_ss);
   Half2<T, V> x, w, c, sn;
   x.load(x0 + (int64_t)h * (b.isq ? a.q_hs : a.k_hs) + d, half);
@@ -201,10 +215,10 @@ __global__ __launch_bounds__(64) void qk_norm_rope_fwd_kernel(QkRopeArgs a, int 
     o.lo[i] = Rnd<T>::one(n0 * c.lo[i]) + Rnd<T>::one(-n1 * sn.lo[i]);   // rounded by the store
     o.hi[i] = Rnd<T>::one(n1 * c.hi[i]) + Rnd<T>::one(n0 * sn.hi[i]);
   }
-  T *out = reinterpret_cast<T *>(b.isq ? a.qo : a.ko) + (int64_t)s * (b.isq ? a.qo_ss : a.ko_ss) +
+  T *out = reinterpret_cast<T *>(b.isq ? a.qo : a.ko) + (int64_t)so * (b.isq ? a.qo_ss : a.ko_ss) +
            (int64_t)h * (b.isq ? a.qo_hs : a.ko_hs) + d;
   if (on) o.store(out, half);
-  if (j == 0) a.rstd[(int64_t)s * (a.Hq + a.Hkv) + b.rstd0 + h] = r;
+  if (j == 0 && a.rstd) a.rstd[(int64_t)so * (a.Hq + a.Hkv) + b.rstd0 + h] = r;
 }
 
 template <typename T, int V>
@@ -263,7 +277,7 @@ bool vec_ok(const QkRopeArgs &a, bool backward, int V, int eb) {
   if ((a.D / 2) % V != 0) return false;
   const int vb = V * eb;
   for (const void *p : {a.q, a.k, a.qw, a.kw, a.cos, a.sin, (const void *)a.qo, (const void *)a.ko, a.dqo, a.dko,
-                        (const void *)a.dq, (const void *)a.dk})
+                        (const void *)a.dq, (const void *)a.dk, a.v, (const void *)a.vo})
     if (!aligned(p, vb)) return false;
   for (int64_t s : {a.q_ss, a.q_hs, a.k_ss, a.k_hs, a.cs_ss})
     if (s % V) return false;
@@ -271,7 +285,7 @@ bool vec_ok(const QkRopeArgs &a, bool backward, int V, int eb) {
     for (int64_t s : {a.dqo_ss, a.dqo_hs, a.dko_ss, a.dko_hs, a.dq_ss, a.dq_hs, a.dk_ss, a.dk_hs})
       if (s % V) return false;
   } else {
-    for (int64_t s : {a.qo_ss, a.qo_hs, a.ko_ss, a.ko_hs})
+    for (int64_t s : {a.qo_ss, a.qo_hs, a.ko_ss, a.ko_hs, a.v_ss, a.v_hs, a.vo_ss, a.vo_hs})
       if (s % V) return false;
   }
   return true;
@@ -283,7 +297,8 @@ void launch_v(const QkRopeArgs &a, bool backward, hipStream_t st) {
   int lg = 0;
   while ((1 << lg) * V < half) ++lg;   // half <= 64, so G = 1 << lg <= 64
   const int ngrp = 64 >> lg;
-  const int nblk = (a.Hq + ngrp - 1) / ngrp + (a.Hkv + ngrp - 1) / ngrp;
+  const int nbk = (a.Hkv + ngrp - 1) / ngrp;
+  const int nblk = (a.q ? (a.Hq + ngrp - 1) / ngrp : 0) + nbk + (!backward && a.v ? nbk : 0);
   const dim3 grid((unsigned)a.S, (unsigned)nblk), block(64);
   const float inv_d = 1.f / (float)a.D;
   if (backward) hipLaunchKernelGGL((qk_norm_rope_bwd_kernel<T, V>), grid, block, 0, st, a, lg, inv_d);

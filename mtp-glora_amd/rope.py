@@ -22,7 +22,11 @@ asking for a norm-weight gradient here is an error).
 ``qwen3_attention_forward`` is Qwen3Attention.forward with those lines replaced
 by ``qk_norm_rope``; everything else (projections, the cache update, the
 attention function looked up in ALL_ATTENTION_FUNCTIONS, o_proj) is called as
-the reference calls it.
+the reference calls it. With a ``StreamingKVCache`` the same launch also
+writes the post-RoPE keys and the values into the cache rows the update would
+fill (``qk_norm_rope_stage``), so the update copies nothing; committing the
+chunk's regular rows then re-runs the kernel on the projections' regular rows
+(the staged rows are the gather's destination, so they cannot be its source).
 """
 from __future__ import annotations
 
@@ -31,6 +35,7 @@ import sys
 import torch
 
 from . import _lib
+from .cache import StreamingKVCache
 from .ops import _dev, _stream, dtype_code
 
 
@@ -113,6 +118,131 @@ def norm_rope_backward(q, k, q_weight, k_weight, cos, sin, rstd, grad_q, grad_k)
     return dq, dk
 
 
+def _dst(name: str, t: torch.Tensor, S: int, H: int, D: int, dtype):
+    """(token stride, head stride) of a [1, H, S, D] destination view."""
+    _dev(name, t)
+    if tuple(t.shape) != (1, H, S, D) or t.stride(3) != 1 or t.dtype != dtype:
+        raise ValueError(f"{name}: expected a [1, {H}, {S}, {D}] {dtype} view with unit stride on D, got "
+                         f"{tuple(t.shape)} {t.dtype} strides {t.stride()}")
+    return t.stride(2), t.stride(1)
+
+
+def norm_rope_stage_forward(q, k, v, q_weight, k_weight, cos, sin, eps: float, k_dst, v_dst,
+                            rows: torch.Tensor | None = None):
+    """One launch: q / k norm + RoPE as ``norm_rope_forward``, with the key
+    embeddings written into ``k_dst`` and v copied into ``v_dst`` ([1, Hkv, S,
+    D] views, e.g. KV-cache rows). q may be None (keys and values only). With
+    ``rows`` (int32 [n]) output row s takes input row rows[s] (gather; n rows
+    written). Returns (q_embed [1, S, Hq, D] or None, rstd or None)."""
+    k3, v3 = _heads("key_states", k), _heads("value_states", v)
+    S_in, Hkv, D = k3.shape
+    if tuple(v3.shape) != (S_in, Hkv, D):
+        raise ValueError(f"value_states {tuple(v.shape)} does not match key_states {tuple(k.shape)}")
+    c, s = _table("cos", cos, S_in, D), _table("sin", sin, S_in, D)
+    if c.stride(0) != s.stride(0):
+        c, s = c.contiguous(), s.contiguous()
+    _check_dtypes(k3, ("value_states", v3), ("k_weight", k_weight), ("cos", c), ("sin", s))
+    if rows is not None:
+        _dev("rows", rows)
+        if rows.dtype != torch.int32 or rows.dim() != 1 or not rows.is_contiguous():
+            raise TypeError("rows: expected a contiguous int32 vector")
+        S = rows.numel()
+    else:
+        S = S_in
+    kss, khs = _dst("k_dst", k_dst, S, Hkv, D, k3.dtype)
+    vss, vhs = _dst("v_dst", v_dst, S, Hkv, D, k3.dtype)
+    qo = rstd = None
+    qp = qss = qhs = qop = qoss = qohs = 0
+    Hq = 0
+    if q is not None:
+        q3 = _heads("query_states", q)
+        if q3.shape[0] != S_in or q3.shape[2] != D:
+            raise ValueError(f"query_states {tuple(q.shape)} does not match key_states {tuple(k.shape)}")
+        _check_dtypes(k3, ("query_states", q3), ("q_weight", q_weight))
+        Hq = q3.shape[1]
+        qo = torch.empty(1, S, Hq, D, device=k3.device, dtype=k3.dtype)
+        rstd = torch.empty(S, Hq + Hkv, device=k3.device, dtype=torch.float32)
+        qp, qss, qhs, qop, qoss, qohs = q3.data_ptr(), q3.stride(0), q3.stride(1), qo.data_ptr(), qo.stride(1), \
+            qo.stride(2)
+    for name, w in (("q_weight", q_weight), ("k_weight", k_weight)):
+        if w is None and name == "q_weight" and q is None:
+            continue
+        _dev(name, w)
+        if w.dim() != 1 or w.shape[0] != D or w.stride(0) != 1:
+            raise ValueError(f"{name}: expected a contiguous [{D}] weight, got {tuple(w.shape)}")
+    _lib.call("mga_qk_norm_rope_stage_fwd", qp or None, qss, qhs, k3.data_ptr(), k3.stride(0), k3.stride(1),
+              v3.data_ptr(), v3.stride(0), v3.stride(1), q_weight.data_ptr() if q is not None else None,
+              k_weight.data_ptr(), c.data_ptr(), s.data_ptr(), c.stride(0), float(eps),
+              rows.data_ptr() if rows is not None else None, S_in if rows is not None else 0, S, Hq, Hkv, D,
+              dtype_code(k3.dtype), qop or None, qoss, qohs, k_dst.data_ptr(), kss, khs, v_dst.data_ptr(), vss,
+              vhs, rstd.data_ptr() if rstd is not None else None, _stream(k3))
+    return qo, rstd
+
+
+class _Restage:
+    """Re-stages a chunk's regular rows into the cache prefix from the
+    projections (the rows staged in place are overwritten by the gather, so
+    they cannot be its source): the same kernel, keys and values only."""
+
+    def __init__(self, k, v, k_weight, cos, sin, eps):
+        self.args = (k.detach(), v.detach(), k_weight.detach(), cos.detach(), sin.detach(), eps)
+
+    def __call__(self, idx: torch.Tensor, n: int, k_buf: torch.Tensor, v_buf: torch.Tensor, P: int):
+        k, v, kw, cos, sin, eps = self.args
+        if n == 0:
+            return
+        norm_rope_stage_forward(None, k, v, None, kw, cos, sin, eps, k_buf[None, :, P:P + n],
+                                v_buf[None, :, P:P + n], rows=idx[:n])
+
+
+def _alias(t: torch.Tensor) -> torch.Tensor:
+    """A tensor on t's memory (same storage, offset, sizes, strides) that is
+    not an autograd view of it: the cache buffer it lives in is written again
+    through raw pointers (and its version bumped) while the alias is in use."""
+    return torch.empty(0, dtype=t.dtype, device=t.device).set_(t.untyped_storage(), t.storage_offset(),
+                                                               t.size(), t.stride())
+
+
+class _QKNormRopeStage(torch.autograd.Function):
+    """q embed, and the key embeddings / values written straight into the
+    destination rows; returns aliases of those rows whose gradients go back to
+    k / v."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, q_weight, k_weight, cos, sin, eps, k_dst, v_dst):
+        qo, rstd = norm_rope_stage_forward(q, k, v, q_weight, k_weight, cos, sin, eps, k_dst, v_dst)
+        ctx.save_for_backward(q, k, q_weight, k_weight, cos, sin, rstd)
+        return qo.transpose(1, 2), _alias(k_dst), _alias(v_dst)
+
+    @staticmethod
+    def backward(ctx, gq, gk, gv):
+        q, k, q_weight, k_weight, cos, sin, rstd = ctx.saved_tensors
+        dq, dk = norm_rope_backward(q, k, q_weight, k_weight, cos, sin, rstd, gq.transpose(1, 2),
+                                    gk.transpose(1, 2))
+        return (dq if ctx.needs_input_grad[0] else None, dk if ctx.needs_input_grad[1] else None,
+                gv.transpose(1, 2) if ctx.needs_input_grad[2] else None, None, None, None, None, None, None, None)
+
+
+def qk_norm_rope_stage(query_states, key_states, value_states, q_weight, k_weight, cos, sin, eps, cache,
+                       layer_idx: int):
+    """``qk_norm_rope`` for a ``StreamingKVCache`` layer: one kernel writes
+    the post-RoPE keys and the values into the cache rows [P, P + S) and
+    returns (q_embed [1, Hq, S, D], k, v [1, Hkv, S, D] views of those rows);
+    ``cache.update`` given these views copies nothing."""
+    if torch.is_grad_enabled():
+        for name, w in (("q_norm.weight", q_weight), ("k_norm.weight", k_weight)):
+            if w.requires_grad:
+                raise NotImplementedError(f"{name} requires grad; the fused q/k norm computes no weight "
+                                          "gradient (freeze the base model's norm weights)")
+        if cos.requires_grad or sin.requires_grad:
+            raise NotImplementedError("cos / sin require grad; the fused rope computes no gradient for them")
+    k_dst, v_dst = cache.stage_rows(layer_idx, key_states.transpose(1, 2))
+    qe, ke, ve = _QKNormRopeStage.apply(query_states, key_states, value_states, q_weight, k_weight, cos, sin,
+                                        eps, k_dst, v_dst)
+    ke._mga_restage = _Restage(key_states, value_states, k_weight, cos, sin, eps)
+    return qe, ke, ve
+
+
 class _QKNormRope(torch.autograd.Function):
     @staticmethod
     def forward(ctx, q, k, q_weight, k_weight, cos, sin, eps):
@@ -176,9 +306,16 @@ def qwen3_attention_forward(self, hidden_states: torch.Tensor, position_embeddin
     if self.q_norm.variance_epsilon != self.k_norm.variance_epsilon:
         raise ValueError("q_norm and k_norm epsilons differ")
     cos, sin = position_embeddings
-    query_states, key_states = qk_norm_rope(q.view(hidden_shape), k.view(hidden_shape), self.q_norm.weight,
-                                            self.k_norm.weight, cos, sin, self.q_norm.variance_epsilon)
-    value_states = v.view(hidden_shape).transpose(1, 2)
+    if isinstance(past_key_value, StreamingKVCache):
+        # keys and values go straight into the cache rows [P, P + S): the
+        # update below finds them in place and copies nothing
+        query_states, key_states, value_states = qk_norm_rope_stage(
+            q.view(hidden_shape), k.view(hidden_shape), v.view(hidden_shape), self.q_norm.weight,
+            self.k_norm.weight, cos, sin, self.q_norm.variance_epsilon, past_key_value, self.layer_idx)
+    else:
+        query_states, key_states = qk_norm_rope(q.view(hidden_shape), k.view(hidden_shape), self.q_norm.weight,
+                                                self.k_norm.weight, cos, sin, self.q_norm.variance_epsilon)
+        value_states = v.view(hidden_shape).transpose(1, 2)
 
     if past_key_value is not None:
         cache_kwargs = {"sin": sin, "cos": cos, "cache_position": cache_position}

@@ -94,3 +94,28 @@ def test_noalloc_rejects_oversized_calls_before_device_work(mga):
                                   P, 128, 4096, P, 128, 1024, P, 128, 1024, 0, P, P, P, P, P, P, P, P, P,
                                   1 << 20, 1 << 20, 0, 32, 8, 128, 0, 0.1, 3, None)
     assert rc == mga._lib.MGA_ERR_INVALID and b"workspace" in lib.mga_last_error()
+
+
+def _stage(lib, **kw):
+    P = ctypes.c_void_p(16)
+    a = dict(q=P, k=P, v=P, qw=P, kw=P, cos=P, sin=P, rows=None, src_rows=0, S=8, Hq=4, Hkv=2, D=128, dtype=0,
+             qo=P, ko=P, vo=P, rstd=P)
+    a.update(kw)
+    return lib.mga_qk_norm_rope_stage_fwd(a["q"], 512, 128, a["k"], 256, 128, a["v"], 256, 128, a["qw"], a["kw"],
+                                          a["cos"], a["sin"], 128, ctypes.c_float(1e-6), a["rows"], a["src_rows"],
+                                          a["S"], a["Hq"], a["Hkv"], a["D"], a["dtype"], a["qo"], 512, 128,
+                                          a["ko"], 128, 1024, a["vo"], 128, 1024, a["rstd"], None)
+
+
+@pytest.mark.parametrize("kw", [dict(v=None), dict(vo=None), dict(k=None), dict(ko=None), dict(dtype=9),
+                                dict(D=130), dict(D=7), dict(Hkv=0), dict(q=None),
+                                dict(q=None, qo=None), dict(qw=None), dict(qo=None),
+                                dict(rows=ctypes.c_void_p(64), src_rows=0)])
+def test_stage_invalid_arguments(mga, kw):
+    """mga_qk_norm_rope_stage_fwd: a missing value operand or output, a query
+    output / rstd without a query (the query-less form passes neither), a
+    query without weight or output, bad sizes or a row gather without its
+    source-row count are rejected before any launch."""
+    lib = mga.load_library()
+    assert _stage(lib, **kw) == mga._lib.MGA_ERR_INVALID
+    assert lib.mga_last_error() != b""

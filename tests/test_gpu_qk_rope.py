@@ -176,3 +176,59 @@ def test_argument_errors(mga, dev):
                          torch.ones(256, device=dev, dtype=torch.bfloat16),
                          torch.ones(1, 8, 256, device=dev, dtype=torch.bfloat16),
                          torch.zeros(1, 8, 256, device=dev, dtype=torch.bfloat16))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("P", [0, 77])
+def test_stage_into_cache_matches_update_path(mga, dev, dtype, P):
+    """qk_norm_rope_stage writes the chunk's post-RoPE keys and its values into
+    the cache rows [P, P + S) in the norm / RoPE launch, and update() then
+    copies nothing. Against the copy path (qk_norm_rope, then update's append)
+    on the same inputs: the cache buffers bit-equal after the update, the
+    query embedding and the q / k / v gradients bit-equal, and after
+    commit_regular (the fused path re-stages the regular rows from the
+    projections) the prefix bit-equal again, i.e. equal to the reference's
+    gather + cat of the post-RoPE keys (collator.py:270-287)."""
+    from importlib import import_module
+    rope = import_module("mtp-glora_amd.rope")
+    S, Hq, Hkv, D = 300, 8, 2, 128
+    q, k, qw, kw, cos, sin = make(S, Hq, Hkv, D, dtype, dev, seed=21 + P, pos0=P)
+    g = torch.Generator(device=dev).manual_seed(22 + P)
+    v = torch.randn(1, S, Hkv, D, generator=g, device=dev).to(dtype)
+    kp = torch.randn(1, Hkv, P, D, generator=g, device=dev).to(dtype)
+    vp = torch.randn(1, Hkv, P, D, generator=g, device=dev).to(dtype)
+    regular = torch.rand(S, generator=g, device=dev) < 0.8
+    idx = torch.nonzero(regular).flatten().to(torch.int32)
+    R = idx.numel()
+    up = [torch.randn(shape, generator=g, device=dev).to(dtype) for shape in
+          ((1, Hq, S, D), (1, Hkv, P + S, D), (1, Hkv, P + S, D))]
+    res = []
+    for fused in (False, True):
+        cache = mga.StreamingKVCache(capacity=P + S + 16, num_layers=1)
+        if P:
+            cache.append_prefix([kp], [vp])
+        qg, kg, vg = (t.clone().requires_grad_() for t in (q, k, v))
+        if fused:
+            qe, ke, ve = rope.qk_norm_rope_stage(qg, kg, vg, qw, kw, cos, sin, 1e-6, cache, 0)
+            assert ke.data_ptr() == cache.key_buffer(0)[:, P].data_ptr()
+        else:
+            qe, ke = mga.qk_norm_rope(qg, kg, qw, kw, cos, sin, 1e-6)
+            ve = vg.transpose(1, 2)
+        kf, vf = cache.update(ke, ve, 0)
+        after_update = (cache.key_buffer(0)[:, :P + S].clone(), cache.value_buffer(0)[:, :P + S].clone())
+        torch.autograd.backward([qe, kf, vf], up)
+        cache.commit_regular(idx, R)
+        torch.cuda.synchronize()
+        after_commit = (cache.key_buffer(0)[:, :P + R].clone(), cache.value_buffer(0)[:, :P + R].clone())
+        res.append((qe.detach(), after_update, after_commit, qg.grad, kg.grad, vg.grad, ke.detach()))
+    (q0, u0, c0, *g0, k0), (q1, u1, c1, *g1, _) = res
+    assert torch.equal(q0, q1)
+    for a, b in zip(u0, u1):
+        assert torch.equal(a, b)
+    for a, b in zip(c0, c1):
+        assert torch.equal(a, b)
+    for a, b in zip(g0, g1):
+        assert a is not None and torch.equal(a, b)
+    # the committed prefix is the reference chain: cat(prefix, post-RoPE keys[idx])
+    assert torch.equal(c1[0][:, P:], k0[0][:, idx.long()])
+    assert torch.equal(c1[1][:, P:], v.transpose(1, 2)[0][:, idx.long()])
