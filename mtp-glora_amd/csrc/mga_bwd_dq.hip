@@ -99,6 +99,9 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnArgs a) {
   const int qcode = in ? a.code[row] : kCodePad;
   const int qv = query_v(qcode);
   const int qlim = (qcode == kCodePad || lse == kNegInfD) ? -1 : row + a.P;
+  // keys up to here precede every query of the wave (pad rows are masked by
+  // the ordered compare alone: their qv sits above every key)
+  const int diag = row - l32 + a.P;
 
   TileList tiles = tile_list(a.kv_num, a.kv_idx, a.fkv_num, a.fkv_idx, qt, a.nKV);
   const int npart = tiles.npart;
@@ -113,13 +116,25 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnArgs a) {
   TrOffsets<HD> tro;
   tro.init(lane);
 
-  // K/V tiles go global -> LDS directly (no staging registers)
+  // K/V tiles go global -> LDS directly (no staging registers), addressed by
+  // a scalar row base plus precomputed 32-bit lane offsets
+  DmaLane<HD, kStep> dma;
+  dma.init();
+  const uint32_t lrowK = dma.lane_row(a.k_ss);
+  const uint32_t lrowV = dma.lane_row(a.v_ss);
   KeyCode knext;
   auto load_step = [&](int j, bf16_t *dK, bf16_t *dV) {
     const int kb = step_base(j);
-    if (kb < a.L) {   // a step past the keys is never computed: nothing to load
-      tile_dma<HD, kStep>(dK, reinterpret_cast<const bf16_t *>(kp), a.k_ss, kb, a.L - 1);
-      tile_dma<HD, kStep>(dV, reinterpret_cast<const bf16_t *>(vp), a.v_ss, kb, a.L - 1);
+    const bf16_t *kr = reinterpret_cast<const bf16_t *>(kp) + (int64_t)kb * a.k_ss;
+    const bf16_t *vr = reinterpret_cast<const bf16_t *>(vp) + (int64_t)kb * a.v_ss;
+    if (kb >= a.L) {
+      // a step past the keys is never computed: nothing to load
+    } else if (kb + kStep <= a.L) {
+      dma.issue(dK, kr, a.k_ss, lrowK);
+      dma.issue(dV, vr, a.v_ss, lrowV);
+    } else {
+      dma.issue_clamped(dK, kr, a.k_ss, a.L - kb);
+      dma.issue_clamped(dV, vr, a.v_ss, a.L - kb);
     }
     if (tid < kStep) knext.load(a.code, kb + tid, a.P, a.L);   // converted at store time
   };
@@ -173,14 +188,23 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnArgs a) {
       if (partial) {
         // a real branch: if-converted, full tiles would pay for the masking
         asm volatile("");
-        const int lim = qlim - kbase - 4 * hi;   // causal: key offset (without 4 hi) <= lim
+        if (kbase + kStep - 1 > diag) {   // keys past the wave's first query: causal bound too
+          const int lim = qlim - kbase - 4 * hi;   // causal: key offset (without 4 hi) <= lim
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const i32x4 w4 = *reinterpret_cast<const i32x4 *>(&tW[8 * i + 4 * hi]);
+          for (int i = 0; i < 4; ++i) {
+            const i32x4 w4 = *reinterpret_cast<const i32x4 *>(&tW[8 * i + 4 * hi]);
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const bool ok = (w4[e] >= qv) & (8 * i + e <= lim);
-            sacc[4 * i + e] = ok ? sacc[4 * i + e] : kNegInfD;   // P = exp2(-inf) = 0
+            for (int e = 0; e < 4; ++e) {
+              const bool ok = (w4[e] >= qv) & (8 * i + e <= lim);
+              sacc[4 * i + e] = ok ? sacc[4 * i + e] : kNegInfD;   // P = exp2(-inf) = 0
+            }
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const i32x4 w4 = *reinterpret_cast<const i32x4 *>(&tW[8 * i + 4 * hi]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) sacc[4 * i + e] = w4[e] >= qv ? sacc[4 * i + e] : kNegInfD;
           }
         }
       }

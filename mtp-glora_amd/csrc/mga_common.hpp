@@ -347,13 +347,15 @@ __device__ __forceinline__ TileList tile_list(const int32_t *pnum, const int32_t
 
 namespace mga {
 
-constexpr int kWX = 0x7fffffff;      // ordered-compare value of a regular key / query
+constexpr int kWX = 0x7ffffffe;      // ordered-compare value of a regular key / query
 constexpr int kWPad = -0x7fffffff;   // ordered-compare value of a pad key
+constexpr int kVPad = 0x7fffffff;    // ordered-compare value of a pad query: above every key
 
 // Ordered-compare form of the MTP predicate: allowed(q, k) = (k <= qlim(q)) &
 // (key_w(k) >= query_v(q)). A mask key at or before the query carries a code
 // (num_prefix_x) no larger than the query's, equal exactly within the query's
 // own block, so one compare replaces "key is regular or in the same block".
+// A pad query sits above every key, so the compare alone masks its row.
 __device__ __forceinline__ int key_w(const int32_t *code, int key, int P, int L) {
   if (key < P) return kWX;
   if (key >= L) return kWPad;
@@ -361,7 +363,9 @@ __device__ __forceinline__ int key_w(const int32_t *code, int key, int P, int L)
   return c == kCodeX ? kWX : (c == kCodePad ? kWPad : c);
 }
 
-__device__ __forceinline__ int query_v(int qcode) { return qcode == kCodeX ? kWX : qcode; }
+__device__ __forceinline__ int query_v(int qcode) {
+  return qcode == kCodeX ? kWX : (qcode == kCodePad ? kVPad : qcode);
+}
 
 // The wave's index within the workgroup as a scalar (wave-uniform) value, so
 // LDS block bases derived from it stay in scalar registers.
@@ -427,16 +431,15 @@ namespace mga {
 // A key's code fetched one step ahead: load() only issues the read (so it does
 // not wait on the tile loads in flight), w() converts at store time.
 struct KeyCode {
-  int raw = 0;
-  int kind = 0;   // 0: chunk key (raw = its code), 1: cached prefix key, 2: past the end
+  int raw = 0;   // the key's code (a cached prefix key reads as regular, a key past the end as pad)
   __device__ __forceinline__ void load(const int32_t *code, int key, int P, int L) {
-    kind = key < P ? 1 : (key >= L ? 2 : 0);
-    if (kind == 0) raw = code[key - P];
+    raw = kCodeX;
+    if (key >= P) raw = key < L ? code[key - P] : kCodePad;
   }
+  // selects, not branches: one conversion per step on the load path
   __device__ __forceinline__ int w() const {
-    if (kind == 1) return kWX;
-    if (kind == 2) return kWPad;
-    return raw == kCodeX ? kWX : (raw == kCodePad ? kWPad : raw);
+    const int v = raw == kCodePad ? kWPad : raw;
+    return raw == kCodeX ? kWX : v;
   }
 };
 
