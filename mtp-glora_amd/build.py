@@ -64,8 +64,10 @@ def build_library(verbose: bool = False, jobs: int = 4, src_dir=None, out_path=N
     with ThreadPoolExecutor(max_workers=jobs) as ex:
         objs = list(ex.map(compile_one, sources))
     tmp = out.with_suffix(".so.tmp")
+    # --no-undefined: a kernel template whose host launch stub the compiler
+    # dropped must fail here, not when the library is loaded on a GPU box
     cmd = [cc, "-shared", f"--offload-arch={ARCH}", "-fPIC", *map(str, objs), "-o", str(tmp),
-           "-L/opt/rocm/lib", "-lhipblaslt"]
+           "-L/opt/rocm/lib", "-lhipblaslt", "-Wl,--no-undefined"]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr}")

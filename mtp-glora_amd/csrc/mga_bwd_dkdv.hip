@@ -62,24 +62,49 @@ __device__ __forceinline__ f32x16 rows16(const float *t, uint32_t ofs) {
 }
 
 // Global -> LDS staging of a 32 x HD tile (bf16 or fp16) by the 4 waves of a
-// group (w4: the wave within the group, gt: the thread within the group):
-// direct loads, completion on vmcnt; rows past rmax repeat row rmax.
+// group (w4: the wave within the group, wave-uniform): direct loads,
+// completion on vmcnt; rows past rmax repeat row rmax. Addresses are a scalar
+// row base plus a 32-bit lane offset (the lane's row term for the source's
+// stride, precomputed, plus its swizzled granule), as in DmaLane.
 template <int HD>
 struct GroupTile {
   static constexpr int kGranRow = HD / 8;
   static constexpr int kRowsPerInst = 64 / kGranRow;
   static constexpr int kInst = kRows / kRowsPerInst / 4;   // direct loads per wave
+  uint32_t gran[kInst];   // byte offset of the lane's granule in its row, per load
+  int lr;                 // the lane's row within a load's row block
 
-  __device__ __forceinline__ static void load(bf16_t *tile, const bf16_t *src, int64_t ss, int r0, int rmax,
-                                              int w4, int gt) {
-    const int lane = gt & 63, p = lane % kGranRow;
+  __device__ __forceinline__ void init(int w4, int lane) {
+    const int p = lane % kGranRow;
+    lr = lane / kGranRow;
 #pragma unroll
     for (int i = 0; i < kInst; ++i) {
-      const int blk = w4 * kInst + i;
-      const int r = blk * kRowsPerInst + lane / kGranRow;
-      const int c = p ^ swz<HD>(r);
-      const int row = min(r0 + r, rmax);
-      __builtin_amdgcn_global_load_lds(src + (int64_t)row * ss + c * 8, (lds_void *)(tile + blk * 512), 16, 0, 0);
+      const int r = (w4 * kInst + i) * kRowsPerInst + lr;
+      gran[i] = opaque_u32((uint32_t)((p ^ swz<HD>(r)) << 4));
+    }
+  }
+  // byte offset of the lane's row for row stride ss
+  __device__ __forceinline__ uint32_t lane_row(int64_t ss) const { return opaque_u32((uint32_t)(lr * ss * 2)); }
+
+  __device__ __forceinline__ void load(bf16_t *tile, const bf16_t *src, int64_t ss, uint32_t lrow, int r0,
+                                       int rmax, int w4) const {
+    if (r0 + kRows - 1 <= rmax) {
+      const bf16_t *base = src + (int64_t)r0 * ss;
+#pragma unroll
+      for (int i = 0; i < kInst; ++i) {
+        const int blk = w4 * kInst + i;
+        const char *b = reinterpret_cast<const char *>(base + (int64_t)(blk * kRowsPerInst) * ss);
+        __builtin_amdgcn_global_load_lds(b + (opaque_u32(lrow) + gran[i]), (lds_void *)(tile + blk * 512), 16, 0,
+                                         0);
+      }
+    } else {   // the chunk's last rows: clamp per lane
+#pragma unroll
+      for (int i = 0; i < kInst; ++i) {
+        const int blk = w4 * kInst + i;
+        const int row = min(r0 + blk * kRowsPerInst + lr, rmax);
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const char *>(src + (int64_t)row * ss) + gran[i],
+                                         (lds_void *)(tile + blk * 512), 16, 0, 0);
+      }
     }
   }
 };
@@ -111,7 +136,10 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_kernel(AttnArgs a, 
   const int w4 = wave & 3;                  // wave within the group
   const int gt = tid & 255;                 // thread within the group
   const int half = w4 >> 1;                 // 32-key half of the tile
-  const int role = w4 & 1;                  // 0: A (S, P, dV), 1: B (dP, dS, dK)
+  // 0: A (S, P, dV), 1: B (dP, dS, dK). Wave w and wave w + 4 share a SIMD
+  // (a workgroup's waves are placed round-robin), so the groups swap the
+  // roles: every SIMD holds one VALU-heavy A and one lighter B.
+  const int role = (w4 & 1) ^ gr;
   const int pair = gr * 2 + half;
   const int G = a.Hq / a.Hkv;
 
@@ -180,12 +208,16 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_kernel(AttnArgs a, 
   // the start of the step before its own, -> LDS at that step's end
   float rl = 0.f, re = 0.f;
   int rc = kCodePad, rq = 0;
+  const int w4u = __builtin_amdgcn_readfirstlane(w4);
+  GroupTile<HD> gtile;
+  gtile.init(w4u, lane);
+  const uint32_t lrowQ = gtile.lane_row(a.q_ss), lrowD = gtile.lane_row(a.do_ss);
   auto load_tiles = [&](const StepInfo &s, bf16_t *dQ, bf16_t *dD) {
     if (s.flags & 1) {
       const bf16_t *qp = reinterpret_cast<const bf16_t *>(a.q) + s.h * a.q_sh;
       const bf16_t *dop = reinterpret_cast<const bf16_t *>(a.dout) + s.h * a.do_sh;
-      GroupTile<HD>::load(dQ, qp, a.q_ss, s.q0, a.S - 1, w4, gt);
-      GroupTile<HD>::load(dD, dop, a.do_ss, s.q0, a.S - 1, w4, gt);
+      gtile.load(dQ, qp, a.q_ss, lrowQ, s.q0, a.S - 1, w4u);
+      gtile.load(dD, dop, a.do_ss, lrowD, s.q0, a.S - 1, w4u);
     }
   };
   auto load_rows = [&](const StepInfo &s) {
@@ -426,6 +458,13 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_kernel(AttnArgs a, 
     }
   }
 }
+
+// explicit instantiations: clang otherwise drops some host launch stubs of
+// this template, leaving undefined symbols
+template __global__ void attn_bwd_dkdv_kernel<128, bf16_t>(AttnArgs, int, int);
+template __global__ void attn_bwd_dkdv_kernel<64, bf16_t>(AttnArgs, int, int);
+template __global__ void attn_bwd_dkdv_kernel<128, f16_t>(AttnArgs, int, int);
+template __global__ void attn_bwd_dkdv_kernel<64, f16_t>(AttnArgs, int, int);
 
 template <int HD, typename T>
 void dkdv_launch(const AttnArgs &a, hipStream_t st) {
