@@ -2,8 +2,9 @@
 //
 // Same work decomposition as the forward (mga_fwd.hip): a workgroup of 4 waves
 // holds 4 (query head, 32-row block) pairs of one kv head, so each staged K/V
-// tile feeds four heads. Q and dO stay in registers. Per 32-key step each
-// wave computes
+// tile feeds four heads. Q and dO stay in registers. K/V tiles are staged
+// 64 keys at a time (one barrier and one set of direct loads per step); per
+// 32-key block of a step each wave computes
 //   S^T  = K Q^T,  dP^T = V dO^T                    (A operands: K, V rows)
 //   P    = exp2(S^T * scale_log2 - lse_log2)         (0 where masked)
 //   dS^T = P (dP^T - delta)
@@ -22,7 +23,8 @@ namespace mga {
 namespace {
 
 constexpr float kNegInfD = -__builtin_huge_valf();
-constexpr int kStep = 32;
+constexpr int kStep = 64;   // keys per staged step (one barrier, one load set)
+constexpr int kSubKeys = 32;   // keys per compute block (the accumulators hold 32 keys)
 
 __host__ __device__ __forceinline__ int heads_per_wg_dq(int G) { return (G % 4 == 0) ? 4 : (G % 2 == 0 ? 2 : 1); }
 
@@ -147,7 +149,8 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnArgs a) {
 #pragma unroll
   for (int db = 0; db < DB; ++db) dqacc[db] = zero16();
 
-  // one 32-key step reading buffer B while the next step loads into 1 - B
+  // one 64-key step reading buffer B (two 32-key compute blocks) while the
+  // next step loads into 1 - B
   auto run_step = [&](auto bsel, int j) {
     constexpr int B = decltype(bsel)::value;
     const bf16_t *tK = B ? sK1 : sK0;
@@ -157,9 +160,15 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnArgs a) {
     const bool partial = (j / kSub) < npart;
     if (j + 1 < nstep) load_step(j + 1, B ? sK0 : sK1, B ? sV0 : sV1);
 
-    if (kbase < a.L) {
+#pragma unroll
+    for (int kb = 0; kb < kStep / kSubKeys; ++kb) {
+      const int sbase = kbase + kb * kSubKeys;
+      if (sbase >= a.L) break;   // the rest of the step is past the keys
+      const bf16_t *sK = tK + kb * kSubKeys * HD;
+      const bf16_t *sV = tV + kb * kSubKeys * HD;
+      const int *sW = tW + kb * kSubKeys;
       // S^T = K Q^T and dP^T - delta = V dO^T - delta (the accumulator starts at
-      // -delta); register r is key kbase + 8 (r / 4) + 4 hi + r % 4
+      // -delta); register r is key sbase + 8 (r / 4) + 4 hi + r % 4
       f32x16 sacc = zero16(), dpacc;
 #pragma unroll
       for (int r = 0; r < 16; ++r) dpacc[r] = -del;
@@ -168,13 +177,13 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnArgs a) {
       auto rd = [&](const bf16_t *t, int ks) {
         return lds_read8(reinterpret_cast<const bf16_t *>(lds_at(t, krow ^ (uint32_t)(ks << 5))));
       };
-      bf16x8 kc = rd(tK, 0), vc = rd(tV, 0);
+      bf16x8 kc = rd(sK, 0), vc = rd(sV, 0);
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         bf16x8 kn, vn;
         if (ks + 1 < KS) {
-          kn = rd(tK, ks + 1);
-          vn = rd(tV, ks + 1);
+          kn = rd(sK, ks + 1);
+          vn = rd(sV, ks + 1);
         }
         __builtin_amdgcn_sched_barrier(0);
         sacc = mfma32<E>(kc, qf[ks], sacc);
@@ -188,11 +197,11 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnArgs a) {
       if (partial) {
         // a real branch: if-converted, full tiles would pay for the masking
         asm volatile("");
-        if (kbase + kStep - 1 > diag) {   // keys past the wave's first query: causal bound too
-          const int lim = qlim - kbase - 4 * hi;   // causal: key offset (without 4 hi) <= lim
+        if (sbase + kSubKeys - 1 > diag) {   // keys past the wave's first query: causal bound too
+          const int lim = qlim - sbase - 4 * hi;   // causal: key offset (without 4 hi) <= lim
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const i32x4 w4 = *reinterpret_cast<const i32x4 *>(&tW[8 * i + 4 * hi]);
+            const i32x4 w4 = *reinterpret_cast<const i32x4 *>(&sW[8 * i + 4 * hi]);
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
               const bool ok = (w4[e] >= qv) & (8 * i + e <= lim);
@@ -202,7 +211,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnArgs a) {
         } else {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const i32x4 w4 = *reinterpret_cast<const i32x4 *>(&tW[8 * i + 4 * hi]);
+            const i32x4 w4 = *reinterpret_cast<const i32x4 *>(&sW[8 * i + 4 * hi]);
 #pragma unroll
             for (int e = 0; e < 4; ++e) sacc[4 * i + e] = w4[e] >= qv ? sacc[4 * i + e] : kNegInfD;
           }
@@ -217,8 +226,9 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnArgs a) {
                                  dpacc[8 * u + 4], dpacc[8 * u + 5], dpacc[8 * u + 6], dpacc[8 * u + 7]);
 #pragma unroll
         for (int db = 0; db < DB; ++db)
-          dqacc[db] = mfma32<E>(tro.operand(tK, 16 * u, db), dsb, dqacc[db]);
+          dqacc[db] = mfma32<E>(tro.operand(sK, 16 * u, db), dsb, dqacc[db]);
       }
+      __builtin_amdgcn_sched_barrier(0);   // one block's registers at a time
     }
 
     if (j + 1 < nstep) store_step(B ? sK0 : sK1, B ? sV0 : sV1, B ? sW0 : sW1);
