@@ -151,6 +151,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_kernel(AttnArgs a, 
   const int kt = (kh * kKeys) / kBlock;     // block-mask key tile
 
   const int key = kh * kKeys + half * 32 + l32;
+  const int key_last = kh * kKeys + half * 32 + 31;   // the wave's last key
   const int kr = min(key, a.L - 1);
   const int kw = min(key_w(a.code, key, a.P, a.L), kVRegular);
 
@@ -331,15 +332,24 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_kernel(AttnArgs a, 
       if (cur.flags & 2) {
         // a real branch: if-converted, full tiles would pay for the masking
         asm volatile("");
-        const int thr = key - cur.q0 - a.P - 4 * hi;   // causal: row offset (without 4 hi) >= thr
         const int *tc = cb(J % 2);
+        if (cur.q0 + a.P < key_last) {   // some row precedes one of the wave's keys: causal bound too
+          const int thr = key - cur.q0 - a.P - 4 * hi;   // causal: row offset (without 4 hi) >= thr
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const i32x4 qv = *reinterpret_cast<const i32x4 *>(lds_at(tc, rofs + 32 * i));
+          for (int i = 0; i < 4; ++i) {
+            const i32x4 qv = *reinterpret_cast<const i32x4 *>(lds_at(tc, rofs + 32 * i));
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const bool ok = (8 * i + e >= thr) & (kw >= qv[e]);
-            sc[4 * i + e] = ok ? sc[4 * i + e] : 0.f;
+            for (int e = 0; e < 4; ++e) {
+              const bool ok = (8 * i + e >= thr) & (kw >= qv[e]);
+              sc[4 * i + e] = ok ? sc[4 * i + e] : 0.f;
+            }
+          }
+        } else {   // the ordered compare alone (a pad row sits above every key)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const i32x4 qv = *reinterpret_cast<const i32x4 *>(lds_at(tc, rofs + 32 * i));
+#pragma unroll
+            for (int e = 0; e < 4; ++e) sc[4 * i + e] = kw >= qv[e] ? sc[4 * i + e] : 0.f;
           }
         }
       }
