@@ -377,12 +377,14 @@ __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane
 // lane's row term (lrow, bytes) and granule term (gran[i], bytes; the swizzle
 // is linear in the row bits, so it splits into a lane part and an i part)
 // into the 32-bit vector offset. gran does not depend on the row stride, so
-// tiles of different sources share it.
-template <int HD, int NR>
+// tiles of different sources share it. NW waves (the first NW of the
+// workgroup) share the loads of a tile.
+template <int HD, int NR, int NW = 4>
 struct DmaLane {
   static constexpr int kGranRow = HD / 8;
   static constexpr int kRowsPerInst = 64 / kGranRow;
-  static constexpr int kInst = NR / kRowsPerInst / 4;
+  static constexpr int kInst = NR / kRowsPerInst / NW;
+  static_assert(kInst >= 1 && kInst * kRowsPerInst * NW == NR, "tile rows must split evenly over the waves");
   uint32_t gran[kInst];
   __device__ __forceinline__ void init() {
     const int lane = threadIdx.x & 63, w = wave_id();
