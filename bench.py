@@ -23,7 +23,9 @@ durations (HIP events on the launch stream) give the roofline fractions.
 
 ``cpu_baseline``: the reference's CPU path (torch flex_attention eager -- the
 dense math path -- fwd + autograd bwd on the restated MTP mask_mod) on one
-KV-head group (4 query heads, full S and P+S), median of timed runs.
+KV-head group (4 query heads, full S and P+S), median of timed runs; beside
+it, ``compiled_fwd_only``: torch.compile(flex_attention) forward on the same
+sample, which on the CPU serves inference only (no LSE, no backward).
 """
 from __future__ import annotations
 
@@ -343,8 +345,31 @@ def graph_time(torch, fn, n: int, reps: int = 5) -> float:
     return e0.elapsed_time(e1) / (n * reps)
 
 
-def cpu_baseline(cfg: dict, gate_cpu, reps: int, heads: int) -> dict:
-    """The reference's CPU attention path on one KV-head group."""
+def cpu_compiled_fwd(torch, fr, q, k, v, bm, scale: float, reps: int) -> dict:
+    """torch.compile(flex_attention) on the CPU, forward only: Inductor's CPU
+    flex kernel serves inference only (it refuses the LSE output and the
+    backward, [torch]_inductor/kernel/flex/flex_cpu.py:71-74), so this figure
+    is an inference-only forward, not the reference's training path. Compiled
+    in this process (compile_threads = 1: no worker pool is started)."""
+    import torch._inductor.config as icfg
+    from torch.nn.attention.flex_attention import flex_attention
+    icfg.compile_threads = 1
+    fn = torch.compile(flex_attention)
+    with torch.no_grad():
+        t0 = time.perf_counter()
+        fn(q, k, v, block_mask=bm, scale=scale, enable_gqa=True)   # compile + first run
+        compile_s = time.perf_counter() - t0
+        times = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn(q, k, v, block_mask=bm, scale=scale, enable_gqa=True)
+            times.append(time.perf_counter() - t0)
+    return dict(seconds=statistics.median(times), compile_s=compile_s)
+
+
+def cpu_baseline(cfg: dict, gate_cpu, reps: int, heads: int, compiled: bool) -> dict:
+    """The reference's CPU attention path on one KV-head group (and, with
+    ``compiled``, the compiled inference-only forward on the same inputs)."""
     import torch
     from oracle import flex_ref as fr
     threads = min(os.cpu_count() or 1, 16)
@@ -369,6 +394,12 @@ def cpu_baseline(cfg: dict, gate_cpu, reps: int, heads: int) -> dict:
             t0 = time.perf_counter()
             fr.reference_attention(q, k, v, bm, D ** -0.5, do=do)
             times.append(time.perf_counter() - t0)
+    comp = None
+    if compiled:
+        try:
+            comp = cpu_compiled_fwd(torch, fr, q, k, v, bm, D ** -0.5, reps)
+        except Exception as e:   # an Inductor CPU toolchain problem leaves the eager figure standing
+            comp = dict(error=f"{type(e).__name__}: {str(e)[:200]}")
     model = "unknown"
     try:
         for line in open("/proc/cpuinfo"):
@@ -377,7 +408,7 @@ def cpu_baseline(cfg: dict, gate_cpu, reps: int, heads: int) -> dict:
                 break
     except OSError:
         pass
-    return dict(seconds=statistics.median(times), times=times, mask_build_s=mask_s,
+    return dict(seconds=statistics.median(times), times=times, mask_build_s=mask_s, compiled=comp,
                 threads=torch.get_num_threads(), cpu_count=os.cpu_count(), cpu_model=model)
 
 
@@ -622,6 +653,8 @@ def main() -> int:
     ap.add_argument("--config", type=int, default=2, choices=sorted(set(CONFIGS) | set(STREAMS)))
     ap.add_argument("--cpu-reps", type=int, default=3, help="timed runs of the CPU baseline (0 = skip)")
     ap.add_argument("--cpu-heads", type=int, default=4, help="query heads in the CPU sample (one KV group)")
+    ap.add_argument("--cpu-compiled", type=int, default=1,
+                    help="also time the compiled (inference-only) CPU forward on the same sample (0 = skip)")
     ap.add_argument("--phase-iters", type=int, default=20)
     ap.add_argument("--pmc-pass", action="store_true",
                     help="for hardware-counter runs: one known-size calibration copy, then one launch "
@@ -809,7 +842,7 @@ def main() -> int:
         out["north_star"] = north_star_phase(torch, mga, syn, args.north_star_steps, 3)
 
     if args.cpu_reps > 0:
-        cb = cpu_baseline(cfg, chunk0["gate_mask"].cpu(), args.cpu_reps, args.cpu_heads)
+        cb = cpu_baseline(cfg, chunk0["gate_mask"].cpu(), args.cpu_reps, args.cpu_heads, args.cpu_compiled)
         frac = args.cpu_heads / Hq
         cpu_tflops = fl_total * frac / cb["seconds"] / 1e12
         out["cpu_baseline"] = {
@@ -823,6 +856,18 @@ def main() -> int:
             "seconds": round(cb["seconds"], 3), "mask_build_s": round(cb["mask_build_s"], 3),
             "cpu_count": cb["cpu_count"], "cpu_model": cb["cpu_model"],
         }
+        comp = cb["compiled"]
+        if comp is not None:
+            entry = {"label": ("inference-only: torch.compile(flex_attention) forward on the CPU, no LSE "
+                               "and no backward (Inductor's CPU flex kernel refuses both), same inputs "
+                               "and block mask, one KV-head group extrapolated like the value")}
+            if "error" in comp:
+                entry["error"] = comp["error"]
+            else:
+                entry.update({"value": round(fl_fwd * frac / comp["seconds"] / 1e12, 4), "unit": "TFLOP/s",
+                              "seconds": round(comp["seconds"], 4), "compile_s": round(comp["compile_s"], 1),
+                              "gpu_fwd_tflops": out["attention"]["fwd_tflops"]})
+            out["cpu_baseline"]["compiled_fwd_only"] = entry
     print(json.dumps(out), flush=True)
     return 0
 

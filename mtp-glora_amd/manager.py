@@ -16,7 +16,11 @@ before it, i.e. the whole forward and backward of the chunk. Here the
 regular-token index is built when the chunk is prepared, before any of the
 chunk's attention work is queued, and its count is copied to pinned host
 memory behind an event; the carry-over waits on that event only, so the host
-goes on queueing the next chunk's kernels while the backward still runs.
+goes on queueing the next chunk's kernels while the backward still runs. The
+position sanity check (collator.py:251-258) is queued at the same point: a
+mismatch flag formed on the device travels with the count, and the carry-over
+prints the reference's message from it (reading the positions back only when
+the flag is set).
 """
 from __future__ import annotations
 
@@ -37,8 +41,8 @@ class StreamingKVCacheManager:
         self.capacity = int(capacity)
         self.sanity_check = sanity_check
         self.cache: StreamingKVCache | None = None
-        self._count_host: torch.Tensor | None = None
-        self._pending = None   # (mask tensor, its version, idx, event)
+        self._host: torch.Tensor | None = None   # pinned [count, position mismatch]
+        self._pending = None   # (mask tensor, its version, idx, event, position check or None)
 
     def reset_cache(self) -> None:
         """Reset KV cache for a new sequence (buffers stay allocated)."""
@@ -71,26 +75,49 @@ class StreamingKVCacheManager:
         reg = chunk_data.get("regular_token_mask")
         if isinstance(reg, torch.Tensor) and reg.is_cuda:
             idx, cnt = ops.regular_index(reg[0])
-            if self._count_host is None:
-                self._count_host = torch.empty(1, dtype=torch.int32, pin_memory=True)
-            self._count_host.copy_(cnt, non_blocking=True)
+            if self._host is None:
+                self._host = torch.empty(2, dtype=torch.int32, pin_memory=True)
+            pos = chunk_data.get("position_ids") if self.sanity_check else None
+            check = None
+            if isinstance(pos, torch.Tensor) and pos.is_cuda and pos.dim() == 2 and pos.shape[1] == idx.numel():
+                check = (pos, pos._version, self.past_seen_tokens)
+                src = torch.cat([cnt, self._position_mismatch(pos[0], idx, cnt, self.past_seen_tokens)])
+            else:
+                src = cnt
+            self._host[:src.numel()].copy_(src, non_blocking=True)
             event = torch.cuda.Event()
             event.record()
-            self._pending = (reg, reg._version, idx, event)
+            self._pending = (reg, reg._version, idx, event, check)
         return chunk_data
 
-    def _regular_rows(self, reg: torch.Tensor):
-        """(idx, R) of the chunk's regular tokens: from the index
+    @staticmethod
+    def _position_mismatch(pos: torch.Tensor, idx: torch.Tensor, cnt: torch.Tensor, P: int) -> torch.Tensor:
+        """[1] int32 on the device: 1 when the positions of the regular rows are
+        not P, P + 1, ..., P + R - 1 (the check of collator.py:251-258), queued
+        without a host wait."""
+        i = torch.arange(idx.numel(), device=idx.device)
+        valid = i < cnt
+        got = pos[torch.where(valid, idx.long(), 0)]
+        return ((got != i + P) & valid).any().to(torch.int32).reshape(1)
+
+    def _regular_rows(self, reg: torch.Tensor, pos):
+        """(idx, R, mismatch) of the chunk's regular tokens: from the index
         built by ``prepare_data_with_kv_cache`` when it was built for this same,
         unmodified mask (waiting on its event only), else built now with one
-        stream sync, as the reference's nonzero()."""
+        stream sync, as the reference's nonzero(). ``mismatch`` is the queued
+        position check's flag when it was formed for these same, unmodified
+        positions and prefix length, else None."""
         pend, self._pending = self._pending, None
         if pend is not None and pend[0] is reg and pend[1] == reg._version:
-            _, _, idx, event = pend
+            _, _, idx, event, check = pend
             event.synchronize()
-            return idx, int(self._count_host[0])
+            mismatch = None
+            if check is not None and check[0] is pos and check[1] == pos._version \
+                    and check[2] == self.past_seen_tokens:
+                mismatch = bool(self._host[1])
+            return idx, int(self._host[0]), mismatch
         idx, cnt = ops.regular_index(reg[0])
-        return idx, int(cnt.item())
+        return idx, int(cnt.item()), None
 
     def extract_regular_kv_cache_for_next_chunk(self, chunk_data: dict, past_key_values=None):
         """Keep only the chunk's regular-token K/V (detached) behind the cached
@@ -102,13 +129,20 @@ class StreamingKVCacheManager:
                           f"but got batch size: {bsz}")
         if past_key_values is None:
             return None
-        idx, R = self._regular_rows(chunk_data["regular_token_mask"])
+        pos_ids = chunk_data.get("position_ids")
+        idx, R, mismatch = self._regular_rows(chunk_data["regular_token_mask"], pos_ids)
 
-        if self.sanity_check and "position_ids" in chunk_data:
-            pos = chunk_data["position_ids"][0]
-            got = pos[idx[:R].long()]
-            expected = torch.arange(self.past_seen_tokens, self.past_seen_tokens + R, device=pos.device)
-            if not torch.equal(got, expected.to(got.dtype)):
+        if self.sanity_check and pos_ids is not None:
+            pos = pos_ids[0]
+            got = expected = None
+            if mismatch is None:   # no queued flag for these positions: the reference's comparison (waits)
+                got = pos[idx[:R].long()]
+                expected = torch.arange(self.past_seen_tokens, self.past_seen_tokens + R, device=pos.device)
+                mismatch = not torch.equal(got, expected.to(got.dtype))
+            if mismatch:
+                if got is None:
+                    got = pos[idx[:R].long()]
+                    expected = torch.arange(self.past_seen_tokens, self.past_seen_tokens + R, device=pos.device)
                 print("extract_regular_kv_cache_for_next_chunk: Sanity check failed. Position IDs mismatch. "
                       f"Expected: {expected}, Actual: {got}")
                 print(f"self.past_seen_tokens: {self.past_seen_tokens}, num_new_regular_tokens: {R}")

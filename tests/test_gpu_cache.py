@@ -108,6 +108,40 @@ def test_stream_of_chunks_matches_reference(mga, dev):
         assert torch.equal(a, c_) and torch.equal(b, d)
 
 
+def test_position_check_queued_with_the_index(mga, dev, capsys):
+    """The position sanity check of collator.py:251-258 is formed on the device
+    when the chunk is prepared and read with the regular-row count: correct
+    positions print nothing, a wrong position prints the reference's message,
+    and positions changed in place after prepare are compared again."""
+    H, D = 2, 64
+    seq = chunk_layout(180, 16, 4, 0, seed=9)
+    S = len(seq.gate)
+    first_regular = int(np.flatnonzero(seq.regular)[3])
+    for case in ("right", "wrong", "changed"):
+        mgr = mga.StreamingKVCacheManager(capacity=1024)
+        cache = mgr.new_cache(1)
+        pos = torch.tensor(seq.position, device=dev)[None]
+        if case == "wrong":
+            pos[0, first_regular] += 1
+        chunk = {"input_ids": torch.zeros(1, S, dtype=torch.long, device=dev),
+                 "gate_mask": torch.tensor(seq.gate, device=dev)[None],
+                 "regular_token_mask": torch.tensor(seq.regular, device=dev)[None], "position_ids": pos}
+        chunk = mgr.prepare_data_with_kv_cache(chunk)
+        k = torch.randn(1, S, H, D, device=dev).bfloat16().transpose(1, 2)
+        cache.update(k, k + 1, 0)
+        if case == "changed":
+            pos[0, first_regular] += 1
+        capsys.readouterr()
+        mgr.extract_regular_kv_cache_for_next_chunk(chunk, cache)
+        out = capsys.readouterr().out
+        if case == "right":
+            assert out == "" and int(mgr._host[1]) == 0
+        else:
+            assert "Sanity check failed. Position IDs mismatch." in out, case
+            assert int(mgr._host[1]) == (1 if case == "wrong" else 0)
+        assert mgr.past_seen_tokens == int(seq.regular.sum())
+
+
 def test_extract_after_mask_changed_in_place(mga, dev):
     """prepare builds the regular-token index early; a regular_token_mask
     changed in place between prepare and extract (or replaced by another
