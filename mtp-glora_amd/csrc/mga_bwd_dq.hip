@@ -124,6 +124,8 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnArgs a) {
   dma.init();
   const uint32_t lrowK = dma.lane_row(a.k_ss);
   const uint32_t lrowV = dma.lane_row(a.v_ss);
+  const auto rowsK = dma.rows(a.k_ss);
+  const auto rowsV = dma.rows(a.v_ss);
   KeyCode knext;
   auto load_step = [&](int j, bf16_t *dK, bf16_t *dV) {
     const int kb = step_base(j);
@@ -132,8 +134,8 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnArgs a) {
     if (kb >= a.L) {
       // a step past the keys is never computed: nothing to load
     } else if (kb + kStep <= a.L) {
-      dma.issue(dK, kr, a.k_ss, lrowK);
-      dma.issue(dV, vr, a.v_ss, lrowV);
+      dma.issue(dK, kr, rowsK, lrowK);
+      dma.issue(dV, vr, rowsV, lrowV);
     } else {
       dma.issue_clamped(dK, kr, a.k_ss, a.L - kb);
       dma.issue_clamped(dV, vr, a.v_ss, a.L - kb);

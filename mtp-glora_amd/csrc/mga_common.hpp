@@ -413,15 +413,26 @@ struct DmaLane {
       __builtin_amdgcn_global_load_lds(base + o, (lds_void *)(tile + (w * kInst + i) * 512), 16, 0, 0);
     }
   }
+  // Scalar byte offsets for row stride ss: the wave's first row block and the
+  // step to the next load's block. Formed once per kernel, so a load's scalar
+  // address is one 64-bit add instead of a 64-bit multiply.
+  struct Rows {
+    int64_t wave;
+    int64_t inst;
+  };
+  __device__ __forceinline__ static Rows rows(int64_t ss) {
+    return {(int64_t)(wave_id() * kInst * kRowsPerInst) * ss * 2, (int64_t)kRowsPerInst * ss * 2};
+  }
   // rows r0 .. r0 + NR - 1 all exist in the source; rowbase is wave-uniform
-  __device__ __forceinline__ void issue(bf16_t *tile, const bf16_t *rowbase, int64_t ss, uint32_t lrow) const {
-    const int w = wave_id();
+  __device__ __forceinline__ void issue(bf16_t *tile, const bf16_t *rowbase, const Rows &rs, uint32_t lrow) const {
+    const char *blk = reinterpret_cast<const char *>(rowbase) + rs.wave;
+    bf16_t *dst = tile + wave_id() * kInst * 512;
 #pragma unroll
     for (int i = 0; i < kInst; ++i) {
-      const char *blk = reinterpret_cast<const char *>(rowbase + (int64_t)((w * kInst + i) * kRowsPerInst) * ss);
       // formed at the use: hoisted out of a loop, the sums would hold registers
       const uint32_t vo = opaque_u32(lrow) + gran[i];
-      __builtin_amdgcn_global_load_lds(blk + vo, (lds_void *)(tile + (w * kInst + i) * 512), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(blk + vo, (lds_void *)(dst + i * 512), 16, 0, 0);
+      blk += rs.inst;
     }
   }
 };

@@ -124,20 +124,22 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
   dma.init();
   const uint32_t lrowK = dma.lane_row(a.k_ss);
   const uint32_t lrowV = dma.lane_row(a.v_ss);
+  const auto rowsK = dma.rows(a.k_ss);
+  const auto rowsV = dma.rows(a.v_ss);
   KeyCode wkey;
-  auto load_tile = [&](int kb, bf16_t *dst, const T *src, int64_t ss, uint32_t lrow) {
+  auto load_tile = [&](int kb, bf16_t *dst, const T *src, int64_t ss, const auto &rs, uint32_t lrow) {
     if (kb >= a.L) {
       // second half of the last tile, past the keys: never computed, nothing to load
     } else if (kb + kStepKeys <= a.L) {
-      dma.issue(dst, reinterpret_cast<const bf16_t *>(src) + (int64_t)kb * ss, ss, lrow);
+      dma.issue(dst, reinterpret_cast<const bf16_t *>(src) + (int64_t)kb * ss, rs, lrow);
     } else {
       dma.issue_clamped(dst, reinterpret_cast<const bf16_t *>(src) + (int64_t)kb * ss, ss, a.L - kb);
     }
   };
-  auto load_k = [&](int j, bf16_t *dK) { load_tile(step_base(j), dK, kp, a.k_ss, lrowK); };
+  auto load_k = [&](int j, bf16_t *dK) { load_tile(step_base(j), dK, kp, a.k_ss, rowsK, lrowK); };
   auto load_v = [&](int j, bf16_t *dV) {
     const int kb = step_base(j);
-    load_tile(kb, dV, vp, a.v_ss, lrowV);
+    load_tile(kb, dV, vp, a.v_ss, rowsV, lrowV);
     // raw code only: converting it here would wait for the tile loads too
     if (tid < kStepKeys) wkey.load(a.code, kb + tid, a.P, a.L);
   };

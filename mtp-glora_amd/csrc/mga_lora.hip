@@ -251,6 +251,7 @@ __global__ __launch_bounds__(256) void lora_down_ring_kernel(LoraDownArgs a) {
   DmaLane<HD, 32> dx;
   dx.init();
   const uint32_t lrx = dx.lane_row(a.x_rs);
+  const auto rowsx = dx.rows(a.x_rs);
   const uint32_t orow = opaque_u32((uint32_t)(l32 * HD + (((uint32_t)hi ^ swz<HD>(l32)) << 3)) * 2u);
   bf16_t *hr = WRITE_H ? reinterpret_cast<bf16_t *>(a.h) + (int64_t)(row_ok ? row : 0) * a.h_rs : nullptr;
   const uint64_t prow = (uint64_t)(row_ok ? row : 0) * (uint64_t)a.K;
@@ -261,7 +262,7 @@ __global__ __launch_bounds__(256) void lora_down_ring_kernel(LoraDownArgs a) {
   auto issue = [&](int c) {   // chunk c of the share into buffer c % RING (past the share: its last chunk)
     const int col = (cbeg + min(c, nchunks - 1)) * HD;
     bf16_t *tx = sX + (c % RING) * TILE;
-    if (nrows == 32) dx.issue(tx, xb + col, a.x_rs, lrx);
+    if (nrows == 32) dx.issue(tx, xb + col, rowsx, lrx);
     else dx.issue_clamped(tx, xb + col, a.x_rs, nrows);
   };
   auto load_ops = [&](int c, bf16x8 (&op)[2][NB]) {
