@@ -299,7 +299,11 @@ int mga_gated_lora_fwd(const void *x, int64_t x_rs, const void *weight, int64_t 
  * forward kept no dropout output (grad_A then recomputes it from x and the
  * seed; K a multiple of 128). With dropout on, grad_x is written with
  * vector accesses: its start must be 16-byte aligned and its row stride a
- * multiple of 4 (of 8 for the 16-byte path).
+ * multiple of 4 (of 8 for the 16-byte path). grad_y B and grad_y^T t run as
+ * one streaming pass over grad_y each (fp32 split sums added in a fixed
+ * order) when rank <= 128, N is a multiple of 8 and grad_y, lora_B and t
+ * have 16-byte aligned rows (strides multiples of 8); otherwise in
+ * hipBLASLt, as grad_y W is.
  */
 int mga_gated_lora_bwd(const void *grad_y, int64_t gy_rs, const void *x, int64_t x_rs,
                        const void *h, int64_t h_rs, const void *weight, int64_t w_rs,

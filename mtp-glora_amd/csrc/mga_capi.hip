@@ -4,6 +4,7 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <algorithm>
 #include <mutex>
 
 #include "../../include/mtp_glora_amd.h"
@@ -375,17 +376,20 @@ struct LoraWs {
   float *part;
   void *packed;
   float *dapart;
+  float *skpart;
 };
 
 // [hipBLASLt workspace | u = dY B : S x rpad | d_a : S x rpad | A^T : K x rpad
 //  (bf16) | split-K partial sums of the down-projection: 8 x S x 96 fp32 |
 //  lora_A in MFMA-operand order, up to 96 ranks at a time: K / 16 x 3 KB |
-//  split partial sums of grad_A: 16 x rpad x K fp32]
-int64_t lora_ws_bytes(int32_t S, int32_t K, int32_t rank) {
+//  split partial sums of grad_A: 16 x rpad x K fp32 | split partial sums of
+//  lora_B's backward products: 8 x max(S, N) x rpad fp32]
+int64_t lora_ws_bytes(int32_t S, int32_t K, int32_t N, int32_t rank) {
   const int64_t rp = lora_rpad(rank);
   return kBlasWorkspace + 2 * align256((int64_t)S * rp * 2) + align256((int64_t)K * rp * 2) +
          align256((int64_t)8 * S * 96 * 4) + align256((int64_t)K / 16 * 3 * 1024) +
-         align256((int64_t)mga::kDaMaxSplit * rp * K * 4);
+         align256((int64_t)mga::kDaMaxSplit * rp * K * 4) +
+         align256((int64_t)mga::kSkinnyMaxSplit * std::max(S, N) * rp * 4);
 }
 
 LoraWs lora_ws(void *ws, int32_t S, int32_t K, int32_t rank) {
@@ -399,6 +403,8 @@ LoraWs lora_ws(void *ws, int32_t S, int32_t K, int32_t rank) {
   w.part = reinterpret_cast<float *>(static_cast<char *>(w.at) + align256((int64_t)K * rp * 2));
   w.packed = reinterpret_cast<char *>(w.part) + align256((int64_t)8 * S * 96 * 4);
   w.dapart = reinterpret_cast<float *>(static_cast<char *>(w.packed) + align256((int64_t)K / 16 * 3 * 1024));
+  w.skpart = reinterpret_cast<float *>(reinterpret_cast<char *>(w.dapart) +
+                                       align256((int64_t)mga::kDaMaxSplit * rp * K * 4));
   return w;
 }
 
@@ -443,7 +449,7 @@ int blas(const char *fn, bool ta, bool tb, int64_t M, int64_t N, int64_t K, cons
 int64_t mga_gated_lora_workspace_bytes(int32_t S, int32_t K, int32_t N, int32_t rank) {
   (void)N;
   if (S <= 0 || K <= 0 || rank <= 0) return 0;
-  return lora_ws_bytes(S, K, rank);
+  return lora_ws_bytes(S, K, N, rank);
 }
 
 int mga_gated_lora_fwd(const void *x, int64_t x_rs, const void *weight, int64_t w_rs, const void *lora_a,
@@ -461,8 +467,8 @@ int mga_gated_lora_fwd(const void *x, int64_t x_rs, const void *weight, int64_t 
       (rc = check_rows_ld(fn, "output", y, y_rs, N)) || (rc = check_rows_ld(fn, "t", t, t_rs, rp)))
     return rc;
   if (thr > 0 && h && (rc = check_vec_rows(fn, "dropout output h", h, h_rs, K)) != MGA_OK) return rc;
-  if (!workspace || workspace_bytes < lora_ws_bytes(S, K, rank))
-    return fail(MGA_ERR_INVALID, "%s: workspace of %lld bytes needed", fn, (long long)lora_ws_bytes(S, K, rank));
+  if (!workspace || workspace_bytes < lora_ws_bytes(S, K, N, rank))
+    return fail(MGA_ERR_INVALID, "%s: workspace of %lld bytes needed", fn, (long long)lora_ws_bytes(S, K, N, rank));
   const LoraWs w = lora_ws(workspace, S, K, rank);
   hipStream_t st = (hipStream_t)stream;
   // t = T(T(s T(dropout(x) A^T)) gate)
@@ -511,18 +517,34 @@ int mga_gated_lora_bwd(const void *grad_y, int64_t gy_rs, const void *x, int64_t
     return rc;
   }
   if (grad_b && (rc = check_rows_ld(fn, "grad_B", grad_b, gb_rs, rank))) return rc;
-  if (!workspace || workspace_bytes < lora_ws_bytes(S, K, rank))
-    return fail(MGA_ERR_INVALID, "%s: workspace of %lld bytes needed", fn, (long long)lora_ws_bytes(S, K, rank));
+  if (!workspace || workspace_bytes < lora_ws_bytes(S, K, N, rank))
+    return fail(MGA_ERR_INVALID, "%s: workspace of %lld bytes needed", fn, (long long)lora_ws_bytes(S, K, N, rank));
   const LoraWs w = lora_ws(workspace, S, K, rank);
   hipStream_t st = (hipStream_t)stream;
-  // u = dY B, d_a = T(T(u gate) s)  (the gradient at lora_A's output)
-  if ((rc = blas(fn, false, false, S, rank, N, grad_y, gy_rs, lora_b, b_rs, false, w.u, rp, w, st)) != MGA_OK)
+  // u = dY B, d_a = T(T(T(u) gate) s) (the gradient at lora_A's output), and
+  // dB = dY^T t: one streaming pass over dY each (ranks up to 128, 16-byte
+  // rows), else hipBLASLt
+  const bool skinny = rank <= 128 && N % 8 == 0 && aligned16(grad_y) && gy_rs % 8 == 0 && aligned16(lora_b) &&
+                      b_rs % 8 == 0 && aligned16(t) && t_rs % 8 == 0;
+  mga::LoraSkinnyArgs sk = {};
+  sk.dy = grad_y; sk.dy_rs = gy_rs; sk.part = w.skpart; sk.S = S; sk.N = N; sk.rank = rank; sk.rp = (int32_t)rp;
+  if (skinny) {
+    sk.sm = lora_b; sk.sm_rs = b_rs;
+    mga::launch_lora_grad_u(sk, gate, scaling, w.da, rp, st);
+    if ((rc = check_launch(fn)) != MGA_OK) return rc;
+  } else {
+    if ((rc = blas(fn, false, false, S, rank, N, grad_y, gy_rs, lora_b, b_rs, false, w.u, rp, w, st)) != MGA_OK)
+      return rc;
+    mga::launch_lora_scale_rows(w.u, rp, gate, scaling, S, rank, (int32_t)rp, w.da, rp, st);
+    if ((rc = check_launch(fn)) != MGA_OK) return rc;
+  }
+  if (grad_b && skinny) {
+    sk.sm = t; sk.sm_rs = t_rs;
+    mga::launch_lora_grad_b(sk, grad_b, gb_rs, st);
+    if ((rc = check_launch(fn)) != MGA_OK) return rc;
+  } else if (grad_b && (rc = blas(fn, true, false, N, rank, S, grad_y, gy_rs, t, t_rs, false, grad_b, gb_rs, w, st))) {
     return rc;
-  mga::launch_lora_scale_rows(w.u, rp, gate, scaling, S, rank, (int32_t)rp, w.da, rp, st);
-  if ((rc = check_launch(fn)) != MGA_OK) return rc;
-  // dB = dY^T t
-  if (grad_b && (rc = blas(fn, true, false, N, rank, S, grad_y, gy_rs, t, t_rs, false, grad_b, gb_rs, w, st)))
-    return rc;
+  }
   if (grad_x) {
     // the LoRA path's gradient first (through dropout when it is on), then
     // dX = T(dY W + that): the base GEMM accumulates onto it in its epilogue

@@ -118,6 +118,19 @@ struct LoraDaArgs {
   int32_t S, K, rank;
 };
 constexpr int kDaMaxSplit = 16;
+// lora_B's backward products over the streamed dY (mga_lora.hip): dB = dY^T t
+// (small = t [S, >= rank]) and u = dY B (small = lora_B [N, rank]); rank <= 128,
+// rows 16-byte aligned with strides a multiple of 8, N a multiple of 8.
+struct LoraSkinnyArgs {
+  const void *dy; int64_t dy_rs;       // [S, N] bf16
+  const void *sm; int64_t sm_rs;       // t or lora_B
+  float *part;                         // split partial sums [nsplit, lines, rp] fp32
+  int32_t S, N, rank, rp;
+};
+constexpr int kSkinnyMaxSplit = 8;
+void launch_lora_grad_b(const LoraSkinnyArgs &a, void *db, int64_t db_rs, hipStream_t stream);
+void launch_lora_grad_u(const LoraSkinnyArgs &a, const float *gate, float scaling, void *da, int64_t da_rs,
+                        hipStream_t stream);
 void launch_lora_down(const LoraDownArgs &a, hipStream_t stream);
 void launch_lora_da(const LoraDaArgs &a, hipStream_t stream);
 void launch_lora_dx(const LoraDxArgs &a, hipStream_t stream);

@@ -4,8 +4,9 @@
 //   out = base(x) + s * B(A(dropout(x))) * gate
 //
 // The plain GEMMs (x W^T, the rank-r up-projection accumulated into the
-// output, dY W, dY B, dY^T t, d_a^T h) go to hipBLASLt (mga_blas.hip). The
-// kernels here fuse what a library GEMM cannot:
+// output, dY W, and d_a^T h when the forward kept h) go to hipBLASLt
+// (mga_blas.hip). The kernels here fuse what a library GEMM cannot, or stream
+// what it runs far from the HBM bound:
 //
 // * the down-projection t = T(T(s * T(h A^T)) * gate) for every row, h =
 //   dropout(x) drawn on the fly (written out only on request: the backward's
@@ -33,7 +34,12 @@
 //   lora_dx_rows_kernel serves K not a multiple of 128, ranks above 128 and
 //   8-byte-aligned rows: one row per lane, the output's columns along the
 //   lane's registers.
-// * lora_scale_rows_kernel: d_a = T(T(u * gate) * s), u = dY B.
+// * lora_skinny_kernel: lora_B's backward products u = dY B and dB = dY^T t,
+//   each one streaming pass over dY (the rank-r side staged beside it), fp32
+//   split sums added in a fixed order by lora_u_finish_kernel (which also
+//   forms d_a = T(T(T(u) * gate) * s)) and lora_db_finish_kernel.
+// * lora_scale_rows_kernel: d_a = T(T(u * gate) * s), u = dY B, when u comes
+//   from hipBLASLt (ranks above 128, unaligned rows).
 // * lora_transpose_kernel: A^T padded to a multiple of 32 ranks (the dX
 //   kernel's MFMA operand wants rank-contiguous rows).
 //
@@ -49,6 +55,7 @@
 // bits & 0xffff >= thr, element 2j + 1 when bits >> 16 >= thr, thr =
 // round(p * 65536). Kept elements are multiplied by 1 / (1 - p), as
 // torch's dropout does. The backward draws the same bits again.
+#include <algorithm>
 #include <type_traits>
 
 #include "mga_common.hpp"
@@ -689,6 +696,255 @@ __global__ __launch_bounds__(256) void lora_transpose_kernel(const bf16_t *A, in
   }
 }
 
+
+// ---- lora_B's backward: the two skinny products over the streamed dY -------
+// MODE 0: dB^T partials   part[split][n][r] = sum over the split's rows s of dY[s][n] t[s][r]
+// MODE 1: u^T partials    part[split][s][r] = sum over the split's columns n of dY[s][n] B[n][r]
+// HBM-bound on dY (each element read once per product). A workgroup of 4
+// waves owns 64 output lines (columns n for MODE 0, rows s for MODE 1) and a
+// share of the 64-wide chunks of the reduced dimension. Each chunk stages a
+// 64 x 64 dY tile (rows s, columns n, swizzled) and the chunk's 64 rows of the
+// small matrix (t for MODE 0, B for MODE 1) as compact rows of RP = 32 RB
+// elements, in a ring of four named buffers (three chunks ahead) filled with
+// direct loads. Every wave issues the same loads per chunk, and every load in
+// flight is a direct load, so the waits name exact counts. Wave w takes
+// k-step w (16 of the 64) of every chunk for all (rank block, line block)
+// outputs:
+//   MODE 0: dB^T[r][n] += t^T[r][s] dY[s][n]      A: t^T, B: dY  (transposed LDS reads)
+//   MODE 1: u^T[r][s]  += B^T[r][n] dY^T[n][s]    A: B^T (transposed read), B: dY rows (8-byte reads)
+// so a lane holds one output line and 16 ranks of each rank block, written
+// as 16-byte runs. The waves' sums are added in a fixed order at the end.
+// Rank columns past the rank and lines past the end hold junk that no
+// finishing kernel reads; reduced-dimension entries past the end are zeroed
+// in an operand. CLAMP (S or N not a multiple of 64) clamps each lane's rows
+// and columns at the edges; without it every address is a wave-uniform base
+// plus a loop-invariant lane offset, which also keeps the compiler from
+// waiting on loads in flight whose address registers a later read would reuse.
+template <int MODE, int RB, bool CLAMP>
+__global__ __launch_bounds__(256, 2) void lora_skinny_kernel(LoraSkinnyArgs a) {
+  constexpr int RP = 32 * RB;                 // compact small-tile row (elements)
+  constexpr int YT = 64 * 64, MT = 64 * RP;
+  constexpr int MG = RP / 8;                  // granules per small-tile row
+  constexpr int MI = 64 * MG / 256;           // small-tile loads per thread (1 .. 4)
+  constexpr int NL = 2 + MI;                  // loads per thread per chunk
+  __shared__ __attribute__((aligned(16))) bf16_t sY0[YT], sY1[YT], sY2[YT], sY3[YT];
+  __shared__ __attribute__((aligned(16))) bf16_t sM0[MT], sM1[MT], sM2[MT], sM3[MT];
+  const int w = wave_id(), tid = threadIdx.x, lane = tid & 63;
+  const int l32 = lane & 31, hi = lane >> 5;
+  const int line0 = blockIdx.x * 64;
+  const int nlines = MODE == 0 ? a.N : a.S;   // output lines
+  const int kdim = MODE == 0 ? a.S : a.N;     // reduced dimension
+  const int nall = (kdim + 63) / 64;
+  const int c0 = (int)((int64_t)nall * blockIdx.y / gridDim.y);
+  const int nch = (int)((int64_t)nall * (blockIdx.y + 1) / gridDim.y) - c0;
+  const bf16_t *dy = reinterpret_cast<const bf16_t *>(a.dy);
+  const bf16_t *sm = reinterpret_cast<const bf16_t *>(a.sm);
+  // granules of a small-matrix row that hold rank columns (a slot past them
+  // reads the last one again: its columns are never used)
+  const int mg_last = (a.rank + 7) / 8 - 1;
+
+  // Per-lane sources. dY tile: 8 granules per row, 8 rows per load, wave w
+  // loads rows 16 w .. 16 w + 15 (two loads). Small tile: MG granules per row,
+  // load i of thread t fills slot 256 i + t (row slot / MG, granule slot % MG).
+  const int yp = lane & 7, yr = lane >> 3;
+  int mrow[MI], mgr[MI];
+#pragma unroll
+  for (int i = 0; i < MI; ++i) {
+    const int slot = 256 * i + tid;
+    mrow[i] = slot / MG;
+    mgr[i] = min(slot % MG, mg_last);
+  }
+  // full chunks: a wave-uniform base plus these 32-bit lane offsets (bytes)
+  uint32_t yo[2], mo[MI];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int r = 16 * w + 8 * i + yr;
+    yo[i] = opaque_u32((uint32_t)((r * a.dy_rs + 8 * (yp ^ swz<64>(r))) * 2));
+  }
+#pragma unroll
+  for (int i = 0; i < MI; ++i) mo[i] = opaque_u32((uint32_t)((mrow[i] * a.sm_rs + 8 * mgr[i]) * 2));
+  // Workgroups start their share at different chunks (rotated by the line
+  // block), so that the many workgroups streaming the same share at the same
+  // time do not all read the same rows of the small matrix at once.
+  const int rot = blockIdx.x % nch;
+  auto chunk_of = [&](int c) { const int r = c + rot; return c0 + (r >= nch ? r - nch : r); };
+  auto issue = [&](int c, bf16_t *tY, bf16_t *tM) {
+    const int cc = chunk_of(min(c, nch - 1));   // past the share: the share's last chunk again
+    const int k0 = cc * 64;
+    const int yrow0 = MODE == 0 ? k0 : line0, ycol0 = MODE == 0 ? line0 : k0;
+    bf16_t *dY = tY + 16 * w * 64;
+    if (!CLAMP || (yrow0 + 64 <= a.S && ycol0 + 64 <= a.N)) {
+      const char *b = reinterpret_cast<const char *>(dy + (int64_t)yrow0 * a.dy_rs + ycol0);
+#pragma unroll
+      for (int i = 0; i < 2; ++i) __builtin_amdgcn_global_load_lds(b + yo[i], (lds_void *)(dY + 8 * i * 64), 16, 0, 0);
+    } else {   // rows past S repeat the last row, columns past N the last granule
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int r = 16 * w + 8 * i + yr;
+        const int g = yp ^ swz<64>(r);
+        const int srow = min(yrow0 + r, a.S - 1), ncol = min(ycol0 + 8 * g, a.N - 8);
+        __builtin_amdgcn_global_load_lds(dy + (int64_t)srow * a.dy_rs + ncol, (lds_void *)(dY + 8 * i * 64), 16, 0, 0);
+      }
+    }
+    if (!CLAMP || k0 + 64 <= kdim) {
+      const char *b = reinterpret_cast<const char *>(sm + (int64_t)k0 * a.sm_rs);
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+        __builtin_amdgcn_global_load_lds(b + mo[i], (lds_void *)(tM + 2048 * i + 512 * w), 16, 0, 0);
+    } else {
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+        __builtin_amdgcn_global_load_lds(sm + (int64_t)min(k0 + mrow[i], kdim - 1) * a.sm_rs + 8 * mgr[i],
+                                         (lds_void *)(tM + 2048 * i + 512 * w), 16, 0, 0);
+    }
+  };
+
+  // A operand from a compact k-major tile (rows k, RP columns): lane (l32, hi)
+  // takes column 32 rb + l32 at rows k0 + 4 hi + 0..3 and k0 + 8 + 4 hi + 0..3
+  // (the k order of TrLane), by two transposed reads
+  const int ti = lane & 15;
+  const uint32_t mro[2] = {
+      opaque_u32((uint32_t)(((4 * hi + (ti >> 2)) * RP + 16 * ((lane >> 4) & 1) + 4 * (ti & 3)) * 2)),
+      opaque_u32((uint32_t)(((8 + 4 * hi + (ti >> 2)) * RP + 16 * ((lane >> 4) & 1) + 4 * (ti & 3)) * 2))};
+  auto m_operand = [&](const bf16_t *tM, int k0, int rb) {
+    const char *b = reinterpret_cast<const char *>(tM) + (k0 * RP + 32 * rb) * 2;
+    return join8(lds_tr4(reinterpret_cast<const bf16_t *>(b + mro[0])),
+                 lds_tr4(reinterpret_cast<const bf16_t *>(b + mro[1])));
+  };
+  TrOffsets<64> try_;
+  try_.init(lane);
+  f32x16 acc[RB][2];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) acc[rb][0] = acc[rb][1] = zero16();
+
+  auto compute = [&](int c, const bf16_t *tY, const bf16_t *tM) {
+    const int kb = chunk_of(c) * 64 + 16 * w;        // first reduced index of this wave's k-step
+    const bool tail = CLAMP && kb + 16 > kdim;
+    bf16x8 av[RB], bv[2];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) av[rb] = m_operand(tM, 16 * w, rb);
+    if (MODE == 0) {
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) bv[nb] = try_.operand(tY, 16 * w, nb);
+    } else {
+      // dY row 32 sb + l32, columns 16 w + 4 hi + 0..3 and 16 w + 8 + 4 hi + 0..3
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb) {
+        const int r = 32 * sb + l32;
+        const i32x2 x = *reinterpret_cast<const i32x2 *>(tY + tile_off<64>(r, 2 * w) + 4 * hi);
+        const i32x2 y = *reinterpret_cast<const i32x2 *>(tY + tile_off<64>(r, 2 * w + 1) + 4 * hi);
+        const i32x4 v = {x[0], x[1], y[0], y[1]};
+        bv[sb] = __builtin_bit_cast(bf16x8, v);
+      }
+    }
+    if (tail) {   // reduced entries kb + 4 hi + e and kb + 8 + 4 hi + e past the end are zeroed
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const bool out = kb + 4 * hi + (e & 3) + 8 * (e >> 2) >= kdim;
+        if (MODE == 0) {
+#pragma unroll
+          for (int rb = 0; rb < RB; ++rb) av[rb][e] = out ? (bf16_t)0.f : av[rb][e];
+        } else {
+#pragma unroll
+          for (int sb = 0; sb < 2; ++sb) bv[sb][e] = out ? (bf16_t)0.f : bv[sb][e];
+        }
+      }
+    }
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int lb = 0; lb < 2; ++lb) acc[rb][lb] = mfma32<bf16_t>(av[rb], bv[lb], acc[rb][lb]);
+  };
+
+  // chunk c: its loads landed (the next two chunks' loads may still be in
+  // flight), a bare barrier (every wave's part is in, and the buffer of chunk
+  // c - 1 is free), then the loads of chunk c + 3 and the products of chunk c
+  // (every iteration runs all four chunks, those past the share without
+  // products, so the loads in flight at the loop head are the same on every
+  // path and the compiler adds no wait of its own)
+  auto chunk = [&](auto bsel, int c) {
+    constexpr int B = decltype(bsel)::value;
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * NL));
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    issue(c + 3, B == 0 ? sY3 : (B == 1 ? sY0 : (B == 2 ? sY1 : sY2)),
+          B == 0 ? sM3 : (B == 1 ? sM0 : (B == 2 ? sM1 : sM2)));
+    if (c < nch)
+      compute(c, B == 0 ? sY0 : (B == 1 ? sY1 : (B == 2 ? sY2 : sY3)),
+              B == 0 ? sM0 : (B == 1 ? sM1 : (B == 2 ? sM2 : sM3)));
+  };
+  issue(0, sY0, sM0);
+  issue(1, sY1, sM1);
+  issue(2, sY2, sM2);
+  for (int c = 0; c < nch; c += 4) {
+    chunk(std::integral_constant<int, 0>{}, c);
+    chunk(std::integral_constant<int, 1>{}, c + 1);
+    chunk(std::integral_constant<int, 2>{}, c + 2);
+    chunk(std::integral_constant<int, 3>{}, c + 3);
+  }
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));   // the ring's trailing loads
+  __syncthreads();
+
+  // fixed-order sum of the waves' accumulators through LDS (the ring's dY
+  // buffers, 3 x 16 x 64 floats), then this split's partial: lane = line
+  // 32 lb + l32, registers = ranks 32 rb + 8 (q / 4) + 4 hi + q % 4
+  float *park = reinterpret_cast<float *>(sY0);
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+    for (int lb = 0; lb < 2; ++lb) {
+      if (w > 0)
+#pragma unroll
+        for (int q = 0; q < 16; ++q) park[((w - 1) * 16 + q) * 64 + lane] = acc[rb][lb][q];
+      __syncthreads();
+      if (w == 0) {
+#pragma unroll
+        for (int v = 0; v < 3; ++v)
+#pragma unroll
+          for (int q = 0; q < 16; ++q) acc[rb][lb][q] += park[(v * 16 + q) * 64 + lane];
+        const int line = line0 + 32 * lb + l32;
+        if (line < nlines) {
+          float *out = a.part + ((int64_t)blockIdx.y * nlines + line) * a.rp + 32 * rb + 4 * hi;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const f32x4 v = {acc[rb][lb][4 * i], acc[rb][lb][4 * i + 1], acc[rb][lb][4 * i + 2],
+                             acc[rb][lb][4 * i + 3]};
+            *reinterpret_cast<f32x4 *>(out + 8 * i) = v;
+          }
+        }
+      }
+      __syncthreads();
+    }
+}
+
+// dB[n][r] = T(sum over the splits, in order), r < rank.
+__global__ __launch_bounds__(256) void lora_db_finish_kernel(LoraSkinnyArgs a, int nsplit, bf16_t *db, int64_t db_rs) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)a.N * a.rank) return;
+  const int n = (int)(i / a.rank), r = (int)(i - (int64_t)n * a.rank);
+  float v = 0.f;
+  for (int y = 0; y < nsplit; ++y) v += a.part[((int64_t)y * a.N + n) * a.rp + r];
+  db[(int64_t)n * db_rs + r] = (bf16_t)v;
+}
+
+// d_a[s][r] = T(T(T(u) * gate[s]) * scaling), u = the sum over the splits in
+// order; 0 for rank <= r < rpad. The roundings of the chain dY B (bf16), then
+// lora_scale_rows.
+__global__ __launch_bounds__(256) void lora_u_finish_kernel(LoraSkinnyArgs a, int nsplit, const float *gate,
+                                                            float scaling, bf16_t *da, int64_t da_rs) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)a.S * a.rp) return;
+  const int s = (int)(i / a.rp), r = (int)(i - (int64_t)s * a.rp);
+  float v = 0.f;
+  if (r < a.rank) {
+    for (int y = 0; y < nsplit; ++y) v += a.part[((int64_t)y * a.S + s) * a.rp + r];
+    const float g = gate ? gate[s] : 1.f;
+    v = rnd(rnd(rnd(v) * g) * scaling);
+  }
+  da[(int64_t)s * da_rs + r] = (bf16_t)v;
+}
+
 namespace {
 
 template <int NB>
@@ -793,6 +1049,53 @@ void launch_lora_transpose(const void *A, int64_t a_rs, int32_t rank, int32_t K,
                            int64_t at_rs, hipStream_t st) {
   hipLaunchKernelGGL(lora_transpose_kernel, dim3((unsigned)((K + 31) / 32), (unsigned)(rpad / 32)), dim3(256), 0, st,
                      reinterpret_cast<const bf16_t *>(A), a_rs, rank, K, rpad, reinterpret_cast<bf16_t *>(At), at_rs);
+}
+
+namespace {
+
+// splits of the reduced dimension: about two workgroups per CU, at most
+// kSkinnyMaxSplit, at least one 64-wide chunk each
+int skinny_splits(int lines, int kdim) {
+  const int nblk = (lines + 63) / 64, nch = (kdim + 63) / 64;
+  const int want = (2 * 256 + nblk - 1) / nblk;
+  return std::max(1, std::min({want, kSkinnyMaxSplit, nch}));
+}
+
+template <int MODE, bool CLAMP>
+void launch_skinny_c(const LoraSkinnyArgs &a, const dim3 &grid, hipStream_t st) {
+  switch (a.rp / 32) {
+    case 1: hipLaunchKernelGGL((lora_skinny_kernel<MODE, 1, CLAMP>), grid, dim3(256), 0, st, a); break;
+    case 2: hipLaunchKernelGGL((lora_skinny_kernel<MODE, 2, CLAMP>), grid, dim3(256), 0, st, a); break;
+    case 3: hipLaunchKernelGGL((lora_skinny_kernel<MODE, 3, CLAMP>), grid, dim3(256), 0, st, a); break;
+    default: hipLaunchKernelGGL((lora_skinny_kernel<MODE, 4, CLAMP>), grid, dim3(256), 0, st, a); break;
+  }
+}
+
+template <int MODE>
+void launch_skinny(const LoraSkinnyArgs &a, int nsplit, hipStream_t st) {
+  const int lines = MODE == 0 ? a.N : a.S;
+  const dim3 grid((unsigned)((lines + 63) / 64), (unsigned)nsplit);
+  if (a.S % 64 == 0 && a.N % 64 == 0) launch_skinny_c<MODE, false>(a, grid, st);
+  else launch_skinny_c<MODE, true>(a, grid, st);
+}
+
+}  // namespace
+
+void launch_lora_grad_b(const LoraSkinnyArgs &a, void *db, int64_t db_rs, hipStream_t st) {
+  const int ns = skinny_splits(a.N, a.S);
+  launch_skinny<0>(a, ns, st);
+  const int64_t n = (int64_t)a.N * a.rank;
+  hipLaunchKernelGGL(lora_db_finish_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, a, ns,
+                     reinterpret_cast<bf16_t *>(db), db_rs);
+}
+
+void launch_lora_grad_u(const LoraSkinnyArgs &a, const float *gate, float scaling, void *da, int64_t da_rs,
+                        hipStream_t st) {
+  const int ns = skinny_splits(a.S, a.N);
+  launch_skinny<1>(a, ns, st);
+  const int64_t n = (int64_t)a.S * a.rp;
+  hipLaunchKernelGGL(lora_u_finish_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, a, ns, gate, scaling,
+                     reinterpret_cast<bf16_t *>(da), da_rs);
 }
 
 }  // namespace mga
