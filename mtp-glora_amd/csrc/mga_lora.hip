@@ -721,7 +721,7 @@ __global__ __launch_bounds__(256) void lora_transpose_kernel(const bf16_t *A, in
 // plus a loop-invariant lane offset, which also keeps the compiler from
 // waiting on loads in flight whose address registers a later read would reuse.
 template <int MODE, int RB, bool CLAMP>
-__global__ __launch_bounds__(256, 2) void lora_skinny_kernel(LoraSkinnyArgs a) {
+__device__ __forceinline__ void lora_skinny_body(const LoraSkinnyArgs &a) {
   constexpr int RP = 32 * RB;                 // compact small-tile row (elements)
   constexpr int YT = 64 * 64, MT = 64 * RP;
   constexpr int MG = RP / 8;                  // granules per small-tile row
@@ -918,6 +918,15 @@ __global__ __launch_bounds__(256, 2) void lora_skinny_kernel(LoraSkinnyArgs a) {
     }
 }
 
+template <int MODE, int RB>
+__global__ __launch_bounds__(256, 2) void lora_skinny_kernel(LoraSkinnyArgs a) {
+  lora_skinny_body<MODE, RB, false>(a);
+}
+template <int MODE, int RB>
+__global__ __launch_bounds__(256, 2) void lora_skinny_clamp_kernel(LoraSkinnyArgs a) {
+  lora_skinny_body<MODE, RB, true>(a);
+}
+
 // dB[n][r] = T(sum over the splits, in order), r < rank.
 __global__ __launch_bounds__(256) void lora_db_finish_kernel(LoraSkinnyArgs a, int nsplit, bf16_t *db, int64_t db_rs) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -1061,22 +1070,25 @@ int skinny_splits(int lines, int kdim) {
   return std::max(1, std::min({want, kSkinnyMaxSplit, nch}));
 }
 
-template <int MODE, bool CLAMP>
-void launch_skinny_c(const LoraSkinnyArgs &a, const dim3 &grid, hipStream_t st) {
-  switch (a.rp / 32) {
-    case 1: hipLaunchKernelGGL((lora_skinny_kernel<MODE, 1, CLAMP>), grid, dim3(256), 0, st, a); break;
-    case 2: hipLaunchKernelGGL((lora_skinny_kernel<MODE, 2, CLAMP>), grid, dim3(256), 0, st, a); break;
-    case 3: hipLaunchKernelGGL((lora_skinny_kernel<MODE, 3, CLAMP>), grid, dim3(256), 0, st, a); break;
-    default: hipLaunchKernelGGL((lora_skinny_kernel<MODE, 4, CLAMP>), grid, dim3(256), 0, st, a); break;
-  }
-}
-
 template <int MODE>
 void launch_skinny(const LoraSkinnyArgs &a, int nsplit, hipStream_t st) {
   const int lines = MODE == 0 ? a.N : a.S;
-  const dim3 grid((unsigned)((lines + 63) / 64), (unsigned)nsplit);
-  if (a.S % 64 == 0 && a.N % 64 == 0) launch_skinny_c<MODE, false>(a, grid, st);
-  else launch_skinny_c<MODE, true>(a, grid, st);
+  const dim3 grid((unsigned)((lines + 63) / 64), (unsigned)nsplit), blk(256);
+  if (a.S % 64 == 0 && a.N % 64 == 0) {
+    switch (a.rp / 32) {
+      case 1: hipLaunchKernelGGL((lora_skinny_kernel<MODE, 1>), grid, blk, 0, st, a); break;
+      case 2: hipLaunchKernelGGL((lora_skinny_kernel<MODE, 2>), grid, blk, 0, st, a); break;
+      case 3: hipLaunchKernelGGL((lora_skinny_kernel<MODE, 3>), grid, blk, 0, st, a); break;
+      default: hipLaunchKernelGGL((lora_skinny_kernel<MODE, 4>), grid, blk, 0, st, a); break;
+    }
+  } else {
+    switch (a.rp / 32) {
+      case 1: hipLaunchKernelGGL((lora_skinny_clamp_kernel<MODE, 1>), grid, blk, 0, st, a); break;
+      case 2: hipLaunchKernelGGL((lora_skinny_clamp_kernel<MODE, 2>), grid, blk, 0, st, a); break;
+      case 3: hipLaunchKernelGGL((lora_skinny_clamp_kernel<MODE, 3>), grid, blk, 0, st, a); break;
+      default: hipLaunchKernelGGL((lora_skinny_clamp_kernel<MODE, 4>), grid, blk, 0, st, a); break;
+    }
+  }
 }
 
 }  // namespace
