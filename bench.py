@@ -566,7 +566,7 @@ def pmc_pass(torch, mga, libc, q, k, v, do, kp, cache, chunk0, P, S, R, Hkv, D, 
     return 0
 
 
-def stream_bench(torch, mga, syn, config: int, cfg: dict) -> int:
+def stream_bench(torch, mga, syn, config: int, cfg: dict, cpu_reps: int = 0) -> int:
     """Time one whole chunk stream (all layers, all chunks) through the
     drop-in API after a one-chunk warm-up; credited FLOPs per chunk from that
     chunk's block mask, times the layer count."""
@@ -629,6 +629,31 @@ def stream_bench(torch, mga, syn, config: int, cfg: dict) -> int:
             append_bytes += nl * 2 * R * Hkv * D * 2 * 2
         P += R
     tflops = credited / seconds / 1e12
+    cpu = None
+    if cpu_reps > 0:
+        # the reference's CPU path at the stream's first, middle and last chunk
+        # of one layer, one query head (of one KV-head group), extrapolated
+        samples, P_c = [], 0
+        picks = sorted({0, len(chunks) // 2, len(chunks) - 1})
+        for c, ch in enumerate(chunks):
+            S_c = ch["gate_mask"].shape[1]
+            if c in picks:
+                bm_c = mga.build_mtp_block_mask(ch["gate_mask"], P_c)
+                a_pre, a_cur = tile_areas(bm_c, S_c, P_c + S_c, P_c)
+                fl_layer = Hq * D * (4 * (a_pre + a_cur) + 6 * a_pre + 10 * a_cur)
+                cb = cpu_baseline(dict(P=P_c, D=D), ch["gate_mask"].cpu(), cpu_reps, 1, False)
+                samples.append({"chunk": c, "prefix": P_c, "rows": S_c, "seconds_one_head": round(cb["seconds"], 3),
+                                "tflops": round(fl_layer / Hq / cb["seconds"] / 1e12, 4)})
+                threads = cb["threads"]
+            P_c += int(ch["regular_token_mask"].sum())
+        rate = statistics.mean(x["tflops"] for x in samples)
+        cpu = {"value": round(rate, 4), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+               "sample": (f"torch flex_attention eager fwd+bwd on CPU (restated MTP mask_mod), one query head of "
+                          f"one layer at chunks {picks} of the stream, median of {cpu_reps} runs each; value = the "
+                          f"mean of their credited-FLOP rates"),
+               "extrapolated": (f"x{Hq} heads, x{nl} layers, all {len(chunks)} chunks at the mean rate: "
+                                f"{credited / (rate * 1e12):.0f} s for the stream"),
+               "chunks": samples}
     out = {
         "metric": METRIC, "value": round(tflops, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": 1,
         "warmup": 1, "ms_per_step": round(seconds * 1e3, 2), "higher_is_better": True,
@@ -641,6 +666,8 @@ def stream_bench(torch, mga, syn, config: int, cfg: dict) -> int:
                    "step": "per chunk: block mask; per layer: cache update, attention fwd, bwd; "
                            "then the regular-row commit of every layer (not after the last chunk)"},
     }
+    if cpu is not None:
+        out["cpu_baseline"] = cpu
     print(json.dumps(out), flush=True)
     return 0
 
@@ -687,7 +714,7 @@ def main() -> int:
     torch.cuda.set_device(dev)
 
     if args.config in STREAMS:
-        return stream_bench(torch, mga, syn, args.config, STREAMS[args.config])
+        return stream_bench(torch, mga, syn, args.config, STREAMS[args.config], args.cpu_reps)
 
     cfg = CONFIGS[args.config]
     Hq, Hkv, D, P = cfg["Hq"], cfg["Hkv"], cfg["D"], cfg["P"]
