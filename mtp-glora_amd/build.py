@@ -32,6 +32,9 @@ def hipcc() -> str:
     return cand
 
 
+COMPILE_TIMEOUT_S = 900
+
+
 def lib_path() -> Path:
     return LIB_DIR / LIB_NAME
 
@@ -54,7 +57,12 @@ def build_library(verbose: bool = False, jobs: int = 4, src_dir=None, out_path=N
     def compile_one(src: Path) -> Path:
         obj = objdir / (src.stem + ".o")
         cmd = [cc, *COMMON_FLAGS, *DEVICE_FLAGS, "-c", str(src), "-o", str(obj)]
-        res = subprocess.run(cmd, capture_output=True, text=True)
+        try:
+            # a compiler that loops (it has, on some unrolled kernels) fails
+            # the build instead of holding it forever
+            res = subprocess.run(cmd, capture_output=True, text=True, timeout=COMPILE_TIMEOUT_S)
+        except subprocess.TimeoutExpired:
+            raise RuntimeError(f"hipcc did not finish {src.name} within {COMPILE_TIMEOUT_S} s") from None
         if res.returncode != 0:
             raise RuntimeError(f"hipcc failed on {src.name}:\n{res.stderr}")
         if verbose:
