@@ -17,7 +17,9 @@
 // behind A: A's P crosses LDS under the one barrier per step that also
 // rotates the staging buffers. The Q / dO tiles of step j + 2 are loaded
 // (global -> LDS) while step j computes, their row data one step ahead: four
-// Q buffers (B's dK of step j - 1 reads Q(j - 1)) and four dO buffers. At the end group 1 hands its
+// Q buffers (B's dK of step j - 1 reads Q(j - 1)) and four dO buffers. The
+// two B waves of a group issue all of its loads: A's chain (S, exp, the mask,
+// P, dV) is the longer one, and B waits for it at the barrier anyway. At the end group 1 hands its
 // accumulators to group 0 through LDS and group 0 adds them in a fixed order:
 // dK and dV summed over the G heads without partial sums in global memory or
 // atomics, and bit-for-bit repeatable.
@@ -61,8 +63,8 @@ __device__ __forceinline__ f32x16 rows16(const float *t, uint32_t ofs) {
   return v;
 }
 
-// Global -> LDS staging of a 32 x HD tile (bf16 or fp16) by the 4 waves of a
-// group (w4: the wave within the group, wave-uniform): direct loads,
+// Global -> LDS staging of a 32 x HD tile (bf16 or fp16) by the two B waves
+// of a group (wl: the loading wave, 0 or 1, wave-uniform): direct loads,
 // completion on vmcnt; rows past rmax repeat row rmax. Addresses are a scalar
 // row base plus a 32-bit lane offset (the lane's row term for the source's
 // stride, precomputed, plus its swizzled granule), as in DmaLane.
@@ -70,16 +72,16 @@ template <int HD>
 struct GroupTile {
   static constexpr int kGranRow = HD / 8;
   static constexpr int kRowsPerInst = 64 / kGranRow;
-  static constexpr int kInst = kRows / kRowsPerInst / 4;   // direct loads per wave
+  static constexpr int kInst = kRows / kRowsPerInst / 2;   // direct loads per loading wave
   uint32_t gran[kInst];   // byte offset of the lane's granule in its row, per load
   int lr;                 // the lane's row within a load's row block
 
-  __device__ __forceinline__ void init(int w4, int lane) {
+  __device__ __forceinline__ void init(int wl, int lane) {
     const int p = lane % kGranRow;
     lr = lane / kGranRow;
 #pragma unroll
     for (int i = 0; i < kInst; ++i) {
-      const int r = (w4 * kInst + i) * kRowsPerInst + lr;
+      const int r = (wl * kInst + i) * kRowsPerInst + lr;
       gran[i] = opaque_u32((uint32_t)((p ^ swz<HD>(r)) << 4));
     }
   }
@@ -87,12 +89,12 @@ struct GroupTile {
   __device__ __forceinline__ uint32_t lane_row(int64_t ss) const { return opaque_u32((uint32_t)(lr * ss * 2)); }
 
   __device__ __forceinline__ void load(bf16_t *tile, const bf16_t *src, int64_t ss, uint32_t lrow, int r0,
-                                       int rmax, int w4) const {
+                                       int rmax, int wl) const {
     if (r0 + kRows - 1 <= rmax) {
       const bf16_t *base = src + (int64_t)r0 * ss;
 #pragma unroll
       for (int i = 0; i < kInst; ++i) {
-        const int blk = w4 * kInst + i;
+        const int blk = wl * kInst + i;
         const char *b = reinterpret_cast<const char *>(base + (int64_t)(blk * kRowsPerInst) * ss);
         __builtin_amdgcn_global_load_lds(b + (opaque_u32(lrow) + gran[i]), (lds_void *)(tile + blk * 512), 16, 0,
                                          0);
@@ -100,7 +102,7 @@ struct GroupTile {
     } else {   // the chunk's last rows: clamp per lane
 #pragma unroll
       for (int i = 0; i < kInst; ++i) {
-        const int blk = w4 * kInst + i;
+        const int blk = wl * kInst + i;
         const int row = min(r0 + blk * kRowsPerInst + lr, rmax);
         __builtin_amdgcn_global_load_lds(reinterpret_cast<const char *>(src + (int64_t)row * ss) + gran[i],
                                          (lds_void *)(tile + blk * 512), 16, 0, 0);
@@ -134,7 +136,6 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_kernel(AttnArgs a, 
   const int l32 = lane & 31, hi = lane >> 5;
   const int gr = wave >> 2;                 // group
   const int w4 = wave & 3;                  // wave within the group
-  const int gt = tid & 255;                 // thread within the group
   const int half = w4 >> 1;                 // 32-key half of the tile
   // 0: A (S, P, dV), 1: B (dP, dS, dK). Wave w and wave w + 4 share a SIMD
   // (a workgroup's waves are placed round-robin), so the groups swap the
@@ -209,21 +210,25 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_kernel(AttnArgs a, 
   // the start of the step before its own, -> LDS at that step's end
   float rl = 0.f, re = 0.f;
   int rc = kCodePad, rq = 0;
-  const int w4u = __builtin_amdgcn_readfirstlane(w4);
+  // the B waves (one per key half) stage the group's tiles and row data: A,
+  // whose chain S -> P -> dV is the longer one, issues no global loads
+  const int wlu = __builtin_amdgcn_readfirstlane(half);
   GroupTile<HD> gtile;
-  gtile.init(w4u, lane);
+  gtile.init(wlu, lane);
   const uint32_t lrowQ = gtile.lane_row(a.q_ss), lrowD = gtile.lane_row(a.do_ss);
   auto load_tiles = [&](const StepInfo &s, bf16_t *dQ, bf16_t *dD) {
     if (s.flags & 1) {
       const bf16_t *qp = reinterpret_cast<const bf16_t *>(a.q) + s.h * a.q_sh;
       const bf16_t *dop = reinterpret_cast<const bf16_t *>(a.dout) + s.h * a.do_sh;
-      gtile.load(dQ, qp, a.q_ss, lrowQ, s.q0, a.S - 1, w4u);
-      gtile.load(dD, dop, a.do_ss, lrowD, s.q0, a.S - 1, w4u);
+      gtile.load(dQ, qp, a.q_ss, lrowQ, s.q0, a.S - 1, wlu);
+      gtile.load(dD, dop, a.do_ss, lrowD, s.q0, a.S - 1, wlu);
     }
   };
+  // row data: lanes 0 .. 31 of the B wave of key half 0
+  const bool row_lane = role == 1 && half == 0 && lane < kRows;
   auto load_rows = [&](const StepInfo &s) {
-    if ((s.flags & 1) && gt < kRows) {
-      rq = s.q0 + gt;
+    if ((s.flags & 1) && row_lane) {
+      rq = s.q0 + lane;
       if (rq < a.S) {
         rl = a.lse[(int64_t)s.h * a.S + rq];
         re = a.delta[(int64_t)s.h * a.S + rq];
@@ -232,14 +237,14 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_kernel(AttnArgs a, 
     }
   };
   auto store_rows = [&](const StepInfo &s, float *dL, float *dE, int *dC) {
-    if ((s.flags & 1) && gt < kRows) {
+    if ((s.flags & 1) && row_lane) {
       const bool in = rq < a.S;
       const int code = in ? rc : kCodePad;
       const float lse = in ? rl : kNegInfK;
       const bool none = code == kCodePad || lse == kNegInfK;   // the row sees no key
-      dL[gt] = none ? 0.f : -lse * inv_scale;
-      dE[gt] = in ? -re : 0.f;
-      dC[gt] = none ? kVPadQuery : (code == kCodeX ? kVRegular : code);
+      dL[lane] = none ? 0.f : -lse * inv_scale;
+      dE[lane] = in ? -re : 0.f;
+      dC[lane] = none ? kVPadQuery : (code == kCodeX ? kVRegular : code);
     }
   };
 
@@ -275,11 +280,13 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_kernel(AttnArgs a, 
   StepInfo ring[4] = {{0, 0, 0}, {0, 0, 0}, {0, 0, 0}, {0, 0, 0}};
   ring[0] = info_of(0);
   ring[1] = info_of(1);
-  load_rows(ring[0]);
-  load_tiles(ring[0], sQ0 + gr * TILE, sD0 + gr * TILE);
-  __builtin_amdgcn_s_waitcnt(0);   // this thread's loads of step 0 landed
-  store_rows(ring[0], sL0 + gr * kRows, sE0 + gr * kRows, sC0 + gr * kRows);
-  load_tiles(ring[1], sQ1 + gr * TILE, sD1 + gr * TILE);
+  if (role == 1) {
+    load_rows(ring[0]);
+    load_tiles(ring[0], sQ0 + gr * TILE, sD0 + gr * TILE);
+    __builtin_amdgcn_s_waitcnt(0);   // this thread's loads of step 0 landed
+    store_rows(ring[0], sL0 + gr * kRows, sE0 + gr * kRows, sC0 + gr * kRows);
+    load_tiles(ring[1], sQ1 + gr * TILE, sD1 + gr * TILE);
+  }
   __syncthreads();
 
   // B: dP - delta of the current and the previous step, alternating by step parity
@@ -304,11 +311,13 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_kernel(AttnArgs a, 
 
     // row data of step j + 1 first: vmcnt retires in issue order, and the
     // wait at the end of this step must not cover the tiles of step j + 2
-    if (j + 1 < nsteps) load_rows(nxt1);
+    if constexpr (R == 1) {
+      if (j + 1 < nsteps) load_rows(nxt1);
+    }
     StepInfo nxt2{0, 0, 0};
     if (j + 2 < nsteps) {
       nxt2 = info_of(j + 2);
-      load_tiles(nxt2, qb((J + 2) % 4) + gr * TILE, db_((J + 2) % 4) + gr * TILE);
+      if constexpr (R == 1) load_tiles(nxt2, qb((J + 2) % 4) + gr * TILE, db_((J + 2) % 4) + gr * TILE);
     }
 
     // The products run on every step, inactive ones included (the operands are
@@ -403,13 +412,15 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_kernel(AttnArgs a, 
       }
     }
 
-    if (j + 1 < nsteps) {
-      // this thread's loads of step j + 1 landed (issued one step ago): wait
-      // for all but the tiles of step j + 2 just issued
-      constexpr int n = 2 * GroupTile<HD>::kInst;
-      if (nxt2.flags & 1) __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8));
-      else __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));   // vmcnt(0)
-      store_rows(nxt1, lb((J + 1) % 2) + gr * kRows, eb((J + 1) % 2) + gr * kRows, cb((J + 1) % 2) + gr * kRows);
+    if constexpr (R == 1) {
+      if (j + 1 < nsteps) {
+        // this thread's loads of step j + 1 landed (issued one step ago): wait
+        // for all but the tiles of step j + 2 just issued
+        constexpr int n = 2 * GroupTile<HD>::kInst;
+        if (nxt2.flags & 1) __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8));
+        else __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));   // vmcnt(0)
+        store_rows(nxt1, lb((J + 1) % 2) + gr * kRows, eb((J + 1) % 2) + gr * kRows, cb((J + 1) % 2) + gr * kRows);
+      }
     }
     ring[(J + 2) % 4] = nxt2;
     __syncthreads();
