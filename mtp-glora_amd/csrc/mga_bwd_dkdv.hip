@@ -370,11 +370,22 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_kernel(AttnArgs a, 
       char *pp = reinterpret_cast<char *>(pbuf(J % 2));
       *reinterpret_cast<i32x4 *>(pp + pofs) = pw[0];
       *reinterpret_cast<i32x4 *>(pp + pofs + 1024) = pw[1];
-      // dV^T += dO^T P (16-row slice u, 32-dim block db)
+      // dV^T += dO^T P (16-row slice u, 32-dim block db); the transposed
+      // operands are read three MFMAs ahead (one ahead left the MFMAs waiting
+      // on the LDS latency: 3-5 % slower at config 2)
+      {
+        constexpr int NT = 2 * DB, AH = 3;
+        bf16x8 ow[AH];
 #pragma unroll
-      for (int t = 0; t < 2 * DB; ++t)
-        acc[t % DB] = mfma32<E>(tro.operand(tD, (t / DB) * 16, t % DB), __builtin_bit_cast(bf16x8, pw[t / DB]),
-                             acc[t % DB]);
+        for (int t = 0; t < AH; ++t) ow[t] = tro.operand(tD, (t / DB) * 16, t % DB);
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          bf16x8 nx;
+          if (t + AH < NT) nx = tro.operand(tD, ((t + AH) / DB) * 16, (t + AH) % DB);
+          acc[t % DB] = mfma32<E>(ow[t % AH], __builtin_bit_cast(bf16x8, pw[t / DB]), acc[t % DB]);
+          if (t + AH < NT) ow[t % AH] = nx;
+        }
+      }
     } else {
       f32x16 &dp = dp2[J % 2];
       const f32x16 &dprev = dp2[(J + 1) % 2];
@@ -396,10 +407,19 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_kernel(AttnArgs a, 
                       keep;
         }
       }
+      {
+        constexpr int NT = 2 * DB, AH = 3;
+        bf16x8 ow[AH];
 #pragma unroll
-      for (int t = 0; t < 2 * DB; ++t)
-        acc[t % DB] = mfma32<E>(tro.operand(tQprev, (t / DB) * 16, t % DB), __builtin_bit_cast(bf16x8, dsw[t / DB]),
-                             acc[t % DB]);
+        for (int t = 0; t < AH; ++t) ow[t] = tro.operand(tQprev, (t / DB) * 16, t % DB);
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          bf16x8 nx;
+          if (t + AH < NT) nx = tro.operand(tQprev, ((t + AH) / DB) * 16, (t + AH) % DB);
+          acc[t % DB] = mfma32<E>(ow[t % AH], __builtin_bit_cast(bf16x8, dsw[t / DB]), acc[t % DB]);
+          if (t + AH < NT) ow[t % AH] = nx;
+        }
+      }
       // dP - delta = dO V^T + (-delta)
       dp = rows16(eb(J % 2), rofs);
       bf16x8 op = lds_read8(reinterpret_cast<const bf16_t *>(lds_at(tD, qk[0])));
