@@ -17,9 +17,14 @@
 // behind A: A's P crosses LDS under the one barrier per step that also
 // rotates the staging buffers. The Q / dO tiles of step j + 2 are loaded
 // (global -> LDS) while step j computes, their row data one step ahead: four
-// Q buffers (B's dK of step j - 1 reads Q(j - 1)) and four dO buffers. The
+// step slots of Q and dO tiles (B's dK of step j - 1 reads Q(j - 1)). The
 // two B waves of a group issue all of its loads: A's chain (S, exp, the mask,
-// P, dV) is the longer one, and B waits for it at the barrier anyway. At the end group 1 hands its
+// P, dV) is the longer one, and B waits for it at the barrier anyway. Those
+// loads stay in flight across the step's end: the direct loads and the row
+// loads are inline asm that the compiler does not count, B waits for exactly
+// the loads of step j + 1 (vmcnt), and the per-step barrier carries no memory
+// fence (__syncthreads' release fence would wait for every direct load in
+// flight, since they write LDS). At the end group 1 hands its
 // accumulators to group 0 through LDS and group 0 adds them in a fixed order:
 // dK and dV summed over the G heads without partial sums in global memory or
 // atomics, and bit-for-bit repeatable.
@@ -96,16 +101,14 @@ struct GroupTile {
       for (int i = 0; i < kInst; ++i) {
         const int blk = wl * kInst + i;
         const char *b = reinterpret_cast<const char *>(base + (int64_t)(blk * kRowsPerInst) * ss);
-        __builtin_amdgcn_global_load_lds(b + (opaque_u32(lrow) + gran[i]), (lds_void *)(tile + blk * 512), 16, 0,
-                                         0);
+        dma16(b, opaque_u32(lrow) + gran[i], tile + blk * 512);
       }
     } else {   // the chunk's last rows: clamp per lane
 #pragma unroll
       for (int i = 0; i < kInst; ++i) {
         const int blk = wl * kInst + i;
         const int row = min(r0 + blk * kRowsPerInst + lr, rmax);
-        __builtin_amdgcn_global_load_lds(reinterpret_cast<const char *>(src + (int64_t)row * ss) + gran[i],
-                                         (lds_void *)(tile + blk * 512), 16, 0, 0);
+        dma16(reinterpret_cast<const char *>(src + (int64_t)row * ss) + gran[i], tile + blk * 512);
       }
     }
   }
@@ -123,8 +126,10 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_kernel(AttnArgs a, 
   // objects so the compiler sees that the direct loads into one never alias
   // the reads of another (the step loop is unrolled to make every index a
   // constant)
-  __shared__ __attribute__((aligned(16))) bf16_t sQ0[2 * TILE], sQ1[2 * TILE], sQ2[2 * TILE], sQ3[2 * TILE];
-  __shared__ __attribute__((aligned(16))) bf16_t sD0[2 * TILE], sD1[2 * TILE], sD2[2 * TILE], sD3[2 * TILE];
+  // ([group][Q tile, dO tile]): one object per step slot, so that the
+  // compiler's wait tracking of the direct loads (a few LDS objects) tells
+  // every slot apart
+  __shared__ __attribute__((aligned(16))) bf16_t sT0[4 * TILE], sT1[4 * TILE], sT2[4 * TILE], sT3[4 * TILE];
   // per row of a step ([group][row]): -lse / scale, -delta, ordered-compare value
   __shared__ __attribute__((aligned(16))) float sL0[2 * kRows], sL1[2 * kRows];
   __shared__ __attribute__((aligned(16))) float sE0[2 * kRows], sE1[2 * kRows];
@@ -190,7 +195,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_kernel(AttnArgs a, 
   // is an immediate: Q / dO operand of k-step ks (row l32, granule
   // (2 ks + hi) ^ swz(l32)), the transposed operands, this lane's row data and
   // its pair's P words
-  const uint32_t gofs = (uint32_t)(gr * TILE * 2);
+  const uint32_t gofs = (uint32_t)(gr * 2 * TILE * 2);
   const uint32_t qrow = (uint32_t)(l32 * HD + (((uint32_t)hi ^ swz<HD>(l32)) << 3)) * 2u;
   uint32_t qk[KS];
 #pragma unroll
@@ -216,28 +221,36 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_kernel(AttnArgs a, 
   GroupTile<HD> gtile;
   gtile.init(wlu, lane);
   const uint32_t lrowQ = gtile.lane_row(a.q_ss), lrowD = gtile.lane_row(a.do_ss);
+  // Every B wave issues the same loads on every step, inactive ones included
+  // (an inactive step's StepInfo is zero: head 0, rows from 0, always in
+  // bounds, never read): with a fixed count in flight the compiler's own wait
+  // before the row data's first use is the same vmcnt as the explicit one, so
+  // the tiles of step j + 2 stay in flight across the step's end.
   auto load_tiles = [&](const StepInfo &s, bf16_t *dQ, bf16_t *dD) {
-    if (s.flags & 1) {
-      const bf16_t *qp = reinterpret_cast<const bf16_t *>(a.q) + s.h * a.q_sh;
-      const bf16_t *dop = reinterpret_cast<const bf16_t *>(a.dout) + s.h * a.do_sh;
-      gtile.load(dQ, qp, a.q_ss, lrowQ, s.q0, a.S - 1, wlu);
-      gtile.load(dD, dop, a.do_ss, lrowD, s.q0, a.S - 1, wlu);
-    }
+    const bf16_t *qp = reinterpret_cast<const bf16_t *>(a.q) + s.h * a.q_sh;
+    const bf16_t *dop = reinterpret_cast<const bf16_t *>(a.dout) + s.h * a.do_sh;
+    gtile.load(dQ, qp, a.q_ss, lrowQ, s.q0, a.S - 1, wlu);
+    gtile.load(dD, dop, a.do_ss, lrowD, s.q0, a.S - 1, wlu);
   };
-  // row data: lanes 0 .. 31 of the B wave of key half 0
+  // row data: loaded by every lane of both B waves (clamped rows), stored by
+  // lanes 0 .. 31 of the B wave of key half 0
   const bool row_lane = role == 1 && half == 0 && lane < kRows;
+  // The row loads are inline asm, outside the compiler's wait counting (which
+  // would wait for every load in flight, the tiles of step j + 2 included,
+  // before the values' first use); rows_wait() below is their wait, and it
+  // hands the registers back only after it.
   auto load_rows = [&](const StepInfo &s) {
-    if ((s.flags & 1) && row_lane) {
-      rq = s.q0 + lane;
-      if (rq < a.S) {
-        rl = a.lse[(int64_t)s.h * a.S + rq];
-        re = a.delta[(int64_t)s.h * a.S + rq];
-        rc = a.code[rq];
-      }
-    }
+    rq = (s.flags & 1) ? s.q0 + (lane & 31) : a.S;
+    const int rr = min(rq, a.S - 1);
+    const float *pl = a.lse + ((int64_t)s.h * a.S + rr);
+    const float *pe = a.delta + ((int64_t)s.h * a.S + rr);
+    const int32_t *pc = a.code + rr;
+    asm volatile("global_load_dword %0, %1, off" : "=v"(rl) : "v"(pl) : "memory");
+    asm volatile("global_load_dword %0, %1, off" : "=v"(re) : "v"(pe) : "memory");
+    asm volatile("global_load_dword %0, %1, off" : "=v"(rc) : "v"(pc) : "memory");
   };
   auto store_rows = [&](const StepInfo &s, float *dL, float *dE, int *dC) {
-    if ((s.flags & 1) && row_lane) {
+    if (row_lane) {
       const bool in = rq < a.S;
       const int code = in ? rc : kCodePad;
       const float lse = in ? rl : kNegInfK;
@@ -257,10 +270,10 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_kernel(AttnArgs a, 
   {
     const i32x4 z = {0, 0, 0, 0};
     for (int i = tid; i < 2 * TILE / 8; i += kThreads) {
-      reinterpret_cast<i32x4 *>(sQ0)[i] = z; reinterpret_cast<i32x4 *>(sQ1)[i] = z;
-      reinterpret_cast<i32x4 *>(sQ2)[i] = z; reinterpret_cast<i32x4 *>(sQ3)[i] = z;
-      reinterpret_cast<i32x4 *>(sD0)[i] = z; reinterpret_cast<i32x4 *>(sD1)[i] = z;
-      reinterpret_cast<i32x4 *>(sD2)[i] = z; reinterpret_cast<i32x4 *>(sD3)[i] = z;
+      reinterpret_cast<i32x4 *>(sT0)[i] = z; reinterpret_cast<i32x4 *>(sT1)[i] = z;
+      reinterpret_cast<i32x4 *>(sT2)[i] = z; reinterpret_cast<i32x4 *>(sT3)[i] = z;
+      reinterpret_cast<i32x4 *>(sT0)[i + 2 * TILE / 8] = z; reinterpret_cast<i32x4 *>(sT1)[i + 2 * TILE / 8] = z;
+      reinterpret_cast<i32x4 *>(sT2)[i + 2 * TILE / 8] = z; reinterpret_cast<i32x4 *>(sT3)[i + 2 * TILE / 8] = z;
     }
     for (int i = tid; i < 2 * kRows; i += kThreads) {
       sL0[i] = 0.f; sL1[i] = 0.f; sE0[i] = 0.f; sE1[i] = 0.f; sC0[i] = kVPadQuery; sC1[i] = kVPadQuery;
@@ -269,8 +282,8 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_kernel(AttnArgs a, 
     __syncthreads();
   }
 
-  auto qb = [&](int i) -> bf16_t * { return i == 0 ? sQ0 : (i == 1 ? sQ1 : (i == 2 ? sQ2 : sQ3)); };
-  auto db_ = [&](int i) -> bf16_t * { return i == 0 ? sD0 : (i == 1 ? sD1 : (i == 2 ? sD2 : sD3)); };
+  auto qb = [&](int i) -> bf16_t * { return i == 0 ? sT0 : (i == 1 ? sT1 : (i == 2 ? sT2 : sT3)); };
+  auto db_ = [&](int i) -> bf16_t * { return qb(i) + TILE; };
   auto lb = [&](int i) -> float * { return i == 0 ? sL0 : sL1; };
   auto eb = [&](int i) -> float * { return i == 0 ? sE0 : sE1; };
   auto cb = [&](int i) -> int * { return i == 0 ? sC0 : sC1; };
@@ -282,11 +295,14 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_kernel(AttnArgs a, 
   ring[1] = info_of(1);
   if (role == 1) {
     load_rows(ring[0]);
-    load_tiles(ring[0], sQ0 + gr * TILE, sD0 + gr * TILE);
-    __builtin_amdgcn_s_waitcnt(0);   // this thread's loads of step 0 landed
+    load_tiles(ring[0], qb(0) + gr * 2 * TILE, db_(0) + gr * 2 * TILE);
+    asm volatile("s_waitcnt vmcnt(0)" : "+v"(rl), "+v"(re), "+v"(rc) : : "memory");   // step 0's loads landed
     store_rows(ring[0], sL0 + gr * kRows, sE0 + gr * kRows, sC0 + gr * kRows);
-    load_tiles(ring[1], sQ1 + gr * TILE, sD1 + gr * TILE);
+    load_tiles(ring[1], qb(1) + gr * 2 * TILE, db_(1) + gr * 2 * TILE);
   }
+  // every wave's key operands (and B's step 0 loads) landed: a wait the
+  // compiler sees, so that it knows no tracked load is in flight in the loop
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
 
   // B: dP - delta of the current and the previous step, alternating by step parity
@@ -311,13 +327,12 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_kernel(AttnArgs a, 
 
     // row data of step j + 1 first: vmcnt retires in issue order, and the
     // wait at the end of this step must not cover the tiles of step j + 2
+    const StepInfo nxt2 = info_of(j + 2);
     if constexpr (R == 1) {
-      if (j + 1 < nsteps) load_rows(nxt1);
-    }
-    StepInfo nxt2{0, 0, 0};
-    if (j + 2 < nsteps) {
-      nxt2 = info_of(j + 2);
-      if constexpr (R == 1) load_tiles(nxt2, qb((J + 2) % 4) + gr * TILE, db_((J + 2) % 4) + gr * TILE);
+      load_rows(nxt1);
+      __builtin_amdgcn_sched_barrier(0);
+      load_tiles(nxt2, qb((J + 2) % 4) + gr * 2 * TILE, db_((J + 2) % 4) + gr * 2 * TILE);
+      __builtin_amdgcn_sched_barrier(0);
     }
 
     // The products run on every step, inactive ones included (the operands are
@@ -433,17 +448,14 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_kernel(AttnArgs a, 
     }
 
     if constexpr (R == 1) {
-      if (j + 1 < nsteps) {
-        // this thread's loads of step j + 1 landed (issued one step ago): wait
-        // for all but the tiles of step j + 2 just issued
-        constexpr int n = 2 * GroupTile<HD>::kInst;
-        if (nxt2.flags & 1) __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8));
-        else __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));   // vmcnt(0)
-        store_rows(nxt1, lb((J + 1) % 2) + gr * kRows, eb((J + 1) % 2) + gr * kRows, cb((J + 1) % 2) + gr * kRows);
-      }
+      // this thread's loads of step j + 1 landed (issued one step ago): wait
+      // for all but the tiles of step j + 2 just issued
+      constexpr int n = 2 * GroupTile<HD>::kInst;
+      asm volatile("s_waitcnt vmcnt(%3)" : "+v"(rl), "+v"(re), "+v"(rc) : "n"(n) : "memory");
+      store_rows(nxt1, lb((J + 1) % 2) + gr * kRows, eb((J + 1) % 2) + gr * kRows, cb((J + 1) % 2) + gr * kRows);
     }
     ring[(J + 2) % 4] = nxt2;
-    __syncthreads();
+    lds_barrier();
   };
 
   // four steps per iteration with no exit in between: an exit inside the
@@ -461,11 +473,15 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_kernel(AttnArgs a, 
   };
   if (role == 0) main_loop(std::integral_constant<int, 0>{});
   else main_loop(std::integral_constant<int, 1>{});
+  // the last steps' loads (of steps past the end, into buffers 0 and 1) land
+  // before those buffers take the accumulators
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
 
   // ---- group 1 hands its accumulators to group 0 (the staging buffers are
   // free after the last barrier): wave (half, role) of group 1 writes into
   // buffer [half][role], 16 KB in quads of registers, lane-interleaved ----
-  float *x = reinterpret_cast<float *>(half == 0 ? (role == 0 ? sQ0 : sD0) : (role == 0 ? sQ1 : sD1));
+  float *x = reinterpret_cast<float *>((half == 0 ? sT0 : sT1) + role * 2 * TILE);
   if (gr == 1) {
 #pragma unroll
     for (int db = 0; db < DB; ++db)

@@ -367,6 +367,35 @@ __device__ __forceinline__ int query_v(int qcode) {
   return qcode == kCodeX ? kWX : (qcode == kCodePad ? kVPad : qcode);
 }
 
+// Workgroup barrier without the memory fences of __syncthreads(): the
+// workgroup-scope release fence there waits for every direct global -> LDS
+// load in flight (they write LDS), which would end any prefetch across the
+// barrier. The caller has waited (s_waitcnt vmcnt) for the direct loads the
+// next step reads; this wave's LDS writes are complete at lgkmcnt(0), and the
+// memory clobber keeps the compiler from moving memory accesses across.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// Direct global -> LDS loads of 16 bytes per lane (global_load_lds_dwordx4;
+// M0 holds the LDS address of the 1 KB block the wave writes) issued as
+// inline asm, outside the compiler's wait counting: the caller owns every
+// wait (s_waitcnt vmcnt) before the bytes are read or the buffer is reused.
+// Scalar base plus a 32-bit lane offset, or a per-lane 64-bit address.
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+  return (uint32_t)(size_t)(const __attribute__((address_space(3))) void *)p;
+}
+__device__ __forceinline__ void dma16(const void *sbase, uint32_t voff, const void *lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :
+               : "v"(voff), "s"(sbase), "s"(lds_addr(lds))
+               : "memory", "m0");
+}
+__device__ __forceinline__ void dma16(const void *gaddr, const void *lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :
+               : "v"(gaddr), "s"(lds_addr(lds))
+               : "memory", "m0");
+}
+
 // The wave's index within the workgroup as a scalar (wave-uniform) value, so
 // LDS block bases derived from it stay in scalar registers.
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
