@@ -15,6 +15,22 @@ static_assert(MGA_BWD_DQ == mga::kBwdDq && MGA_BWD_DKDV == mga::kBwdDkDv, "pass 
 static_assert(MGA_DTYPE_BF16 == mga::kDtBf16 && MGA_DTYPE_F32 == mga::kDtF32 && MGA_DTYPE_F16 == mga::kDtF16,
               "dtype codes");
 
+namespace mga {
+
+int device_cu_count() {
+  static int counts[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (counts[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    counts[dev] = n;
+  }
+  return counts[dev];
+}
+
+}  // namespace mga
+
 namespace {
 
 thread_local char g_err[1024] = {0};

@@ -406,17 +406,21 @@ __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane
 // lane's row term (lrow, bytes) and granule term (gran[i], bytes; the swizzle
 // is linear in the row bits, so it splits into a lane part and an i part)
 // into the 32-bit vector offset. gran does not depend on the row stride, so
-// tiles of different sources share it. NW waves (the first NW of the
-// workgroup) share the loads of a tile.
+// tiles of different sources share it. NW waves share the loads of a tile:
+// with more waves in the workgroup, each group of NW consecutive waves stages
+// its own tiles.
 template <int HD, int NR, int NW = 4>
 struct DmaLane {
   static constexpr int kGranRow = HD / 8;
   static constexpr int kRowsPerInst = 64 / kGranRow;
   static constexpr int kInst = NR / kRowsPerInst / NW;
   static_assert(kInst >= 1 && kInst * kRowsPerInst * NW == NR, "tile rows must split evenly over the waves");
+  static_assert((NW & (NW - 1)) == 0, "NW must be a power of two");
+  // the wave's index within its group of NW
+  __device__ __forceinline__ static int gw() { return wave_id() & (NW - 1); }
   uint32_t gran[kInst];
   __device__ __forceinline__ void init() {
-    const int lane = threadIdx.x & 63, w = wave_id();
+    const int lane = threadIdx.x & 63, w = gw();
     const int p = lane % kGranRow;
 #pragma unroll
     for (int i = 0; i < kInst; ++i) {
@@ -432,7 +436,7 @@ struct DmaLane {
   // issue nothing for a tile with no rows): later rows repeat the last one
   __device__ __forceinline__ void issue_clamped(bf16_t *tile, const bf16_t *rowbase, int64_t ss,
                                                 int nvalid) const {
-    const int lane = threadIdx.x & 63, w = wave_id();
+    const int lane = threadIdx.x & 63, w = gw();
     const int p = lane % kGranRow;
     const char *base = reinterpret_cast<const char *>(rowbase);
 #pragma unroll
@@ -450,12 +454,12 @@ struct DmaLane {
     int64_t inst;
   };
   __device__ __forceinline__ static Rows rows(int64_t ss) {
-    return {(int64_t)(wave_id() * kInst * kRowsPerInst) * ss * 2, (int64_t)kRowsPerInst * ss * 2};
+    return {(int64_t)(gw() * kInst * kRowsPerInst) * ss * 2, (int64_t)kRowsPerInst * ss * 2};
   }
   // rows r0 .. r0 + NR - 1 all exist in the source; rowbase is wave-uniform
   __device__ __forceinline__ void issue(bf16_t *tile, const bf16_t *rowbase, const Rows &rs, uint32_t lrow) const {
     const char *blk = reinterpret_cast<const char *>(rowbase) + rs.wave;
-    bf16_t *dst = tile + wave_id() * kInst * 512;
+    bf16_t *dst = tile + gw() * kInst * 512;
 #pragma unroll
     for (int i = 0; i < kInst; ++i) {
       // formed at the use: hoisted out of a loop, the sums would hold registers

@@ -9,7 +9,9 @@
 // (plus one exchange with the lane 32 away) and accumulates O^T += V^T P^T,
 // feeding the probabilities from registers straight into the B operand. V^T
 // comes from the row-major V tile through the LDS transpose read. 32 rows per
-// wave, 2 waves per SIMD.
+// wave, 2 waves per SIMD. A last round of items that would leave half of an
+// XCD's workgroup slots empty runs as 8-wave workgroups instead: two 4-wave
+// groups split one item's tile list and merge through LDS (NG = 2).
 //
 // Software pipeline: the scores of step j + 1 are computed while the softmax
 // of step j runs, in one scheduling region whose MFMAs and VALU instructions
@@ -62,17 +64,26 @@ __host__ __device__ __forceinline__ int heads_per_wg(int G) { return (G % 4 == 0
 
 }  // namespace
 
-template <int HD, typename T>
-__global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
+// NG = 1: 4 waves per workgroup, one item each. NG = 2: 8 waves, two 4-wave
+// groups taking the even and the odd entries of one item's tile list and
+// merging (O, offset, row sum) through LDS at the end, so an item takes
+// about half as long (for a last round of workgroups that would leave half
+// the GPU idle). The launch runs items [k1, k1 + kn) of each XCD's share.
+template <int HD, typename T, int NG>
+__global__ __launch_bounds__(256 * NG, 2) void attn_fwd_kernel(AttnArgs a, int k1, int kn) {
   typedef typename MfmaElem<T>::type E;
   constexpr int KS = HD / 16;          // k-steps of QK^T over head_dim
   constexpr int DB = HD / 32;          // 32-dim blocks of O^T
   constexpr int TILE = kStepKeys * HD; // elements of one K or V step tile
-  __shared__ __attribute__((aligned(16))) bf16_t sK0[TILE], sK1[TILE];
-  __shared__ __attribute__((aligned(16))) bf16_t sV0[TILE], sV1[TILE];
-  __shared__ __attribute__((aligned(16))) int sW0[kStepKeys], sW1[kStepKeys];
+  // [group][TILE]: each 4-wave group stages the K/V tiles of its own keys
+  __shared__ __attribute__((aligned(16))) bf16_t sK0[NG * TILE], sK1[NG * TILE];
+  __shared__ __attribute__((aligned(16))) bf16_t sV0[NG * TILE], sV1[NG * TILE];
+  __shared__ __attribute__((aligned(16))) int sW0[NG * kStepKeys], sW1[NG * kStepKeys];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int grp = NG == 2 ? wave_id() >> 2 : 0;   // the group's entries: grp, grp + NG, ...
+  const int wave = wave_id() & 3;                 // wave within the group
+  const int gtid = tid & 255;
   const int l32 = lane & 31, hi = lane >> 5;
   const int G = a.Hq / a.Hkv;
   const int HPW = heads_per_wg(G);
@@ -82,7 +93,15 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
 
   // logical item: kv head major (one kv head per XCD when Hkv = 8), then query
   // blocks from the last (longest) to the first, then the head slice
-  const int li = xcd_swizzle(blockIdx.x, a.Hkv * nslice * nqb);
+  // item: XCD x = blockIdx % 8 runs the contiguous share x0 .. x0 + n_x - 1
+  // of the logical items (kv head major, longest first), this launch its
+  // entries k1 .. k1 + kn - 1
+  const int n_items = a.Hkv * nslice * nqb;
+  const int xcd = blockIdx.x & 7;
+  const int o = k1 + (int)(blockIdx.x >> 3);
+  const int n_x = n_items / 8 + (xcd < n_items % 8 ? 1 : 0);
+  if (o >= n_x || o >= k1 + kn) return;
+  const int li = xcd * (n_items / 8) + min(xcd, n_items % 8) + o;
   const int g = li / (nslice * nqb);
   const int rem = li % (nslice * nqb);
   const int qb = nqb - 1 - rem / nslice;
@@ -110,15 +129,24 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
 
   TileList tiles = tile_list(a.kv_num, a.kv_idx, a.fkv_num, a.fkv_idx, qt, a.nKV);
   const int npart = tiles.npart;
-  const int nstep = kStepsPerTile * tiles.ntot;
-  auto step_base = [&](int j) { return tiles.at(j / kStepsPerTile) * kBlock + (j % kStepsPerTile) * kStepKeys; };
+  const int nstep = kStepsPerTile * ((tiles.ntot - grp + NG - 1) / NG);   // this group's steps
+  const int nloop = kStepsPerTile * ((tiles.ntot + NG - 1) / NG);        // group 0's (>= group 1's)
+  auto tile_of = [&](int j) { return NG * (j / kStepsPerTile) + grp; };
+  auto step_base = [&](int j) { return tiles.at(tile_of(j)) * kBlock + (j % kStepsPerTile) * kStepKeys; };
 
   // per-lane LDS offsets: K rows (A operand of QK^T) and the V^T transpose reads
   // K operand of k-step ks: row l32 (+ 32 kb), granule (2 ks + hi) ^ swz(l32),
   // i.e. byte offset krow ^ (ks << 5)
-  const uint32_t krow = opaque_u32((uint32_t)(l32 * HD + (((uint32_t)hi ^ swz<HD>(l32)) << 3)) * 2u);
+  const uint32_t gofs = (uint32_t)(grp * TILE * 2);   // the group's part of every tile buffer (bytes)
+  const uint32_t krow = opaque_u32(gofs + (uint32_t)(l32 * HD + (((uint32_t)hi ^ swz<HD>(l32)) << 3)) * 2u);
   TrOffsets<HD> tro;
   tro.init(lane);
+  if constexpr (NG == 2) {
+#pragma unroll
+    for (int sx = 0; sx < 2; ++sx)
+#pragma unroll
+      for (int mb = 0; mb < DB; ++mb) tro.off[sx][mb] = opaque_u32(tro.off[sx][mb] + gofs);
+  }
 
   DmaLane<HD, kStepKeys> dma;   // shared by the K and V tiles
   dma.init();
@@ -131,9 +159,9 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
     if (kb >= a.L) {
       // second half of the last tile, past the keys: never computed, nothing to load
     } else if (kb + kStepKeys <= a.L) {
-      dma.issue(dst, reinterpret_cast<const bf16_t *>(src) + (int64_t)kb * ss, rs, lrow);
+      dma.issue(dst + grp * TILE, reinterpret_cast<const bf16_t *>(src) + (int64_t)kb * ss, rs, lrow);
     } else {
-      dma.issue_clamped(dst, reinterpret_cast<const bf16_t *>(src) + (int64_t)kb * ss, ss, a.L - kb);
+      dma.issue_clamped(dst + grp * TILE, reinterpret_cast<const bf16_t *>(src) + (int64_t)kb * ss, ss, a.L - kb);
     }
   };
   auto load_k = [&](int j, bf16_t *dK) { load_tile(step_base(j), dK, kp, a.k_ss, rowsK, lrowK); };
@@ -141,10 +169,11 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
     const int kb = step_base(j);
     load_tile(kb, dV, vp, a.v_ss, rowsV, lrowV);
     // raw code only: converting it here would wait for the tile loads too
-    if (tid < kStepKeys) wkey.load(a.code, kb + tid, a.P, a.L);
+    if (gtid < kStepKeys) wkey.load(a.code, kb + gtid, a.P, a.L);
   };
   auto store_w = [&](int *dW) {
-    if (tid < kStepKeys) *reinterpret_cast<int *>(const_cast<char *>(lds_at(dW, opaque_u32(tid * 4u)))) = wkey.w();
+    if (gtid < kStepKeys)
+      *reinterpret_cast<int *>(const_cast<char *>(lds_at(dW + grp * kStepKeys, opaque_u32(gtid * 4u)))) = wkey.w();
   };
 
   const float c = a.scale_log2;
@@ -252,13 +281,13 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
     constexpr int B = decltype(bsel)::value;
     const bf16_t *tKn = B ? sK0 : sK1;   // K of step j + 1
     const bf16_t *tV = B ? sV1 : sV0;    // V of step j
-    const int *tW = B ? sW1 : sW0;
+    const int *tW = (B ? sW1 : sW0) + grp * kStepKeys;
     f32x16 (&s)[kStepBlocks] = sacc[B];
     f32x16 (&sn)[kStepBlocks] = sacc[1 - B];
-    const int kbase = step_base(j);
+    const int kbase = j < nstep ? step_base(j) : a.L;   // past the group's steps: idle (barriers only)
     const bool act = kbase < a.L;
     const bool act_n = j + 1 < nstep && step_base(j + 1) < a.L;
-    const bool partial = (j / kStepsPerTile) < npart;
+    const bool partial = tile_of(j) < npart;
     if (j + 2 < nstep) load_k(j + 2, B ? sK1 : sK0);
     if (j + 1 < nstep) load_v(j + 1, B ? sV0 : sV1);
 
@@ -357,9 +386,37 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
   __syncthreads();
   if (nstep > 0) scores(sK0, sacc[0]);   // step 0 always has keys
   __syncthreads();   // every wave is done with sK0 before step 0 loads into it
-  for (int j = 0; j < nstep; j += 2) {
+  for (int j = 0; j < nloop; j += 2) {
     run_step(std::integral_constant<int, 0>{}, j);
-    if (j + 1 < nstep) run_step(std::integral_constant<int, 1>{}, j + 1);
+    if (j + 1 < nloop) run_step(std::integral_constant<int, 1>{}, j + 1);
+  }
+
+  if constexpr (NG == 2) {
+    // group 1 hands its (O^T, offset, row sum) to group 0 through LDS (the
+    // tile buffers are free after the last barrier); group 0 rescales both
+    // to the larger offset and adds them, in a fixed order
+    float *xo = reinterpret_cast<float *>(wave < 2 ? sK0 : sV0) + (wave & 1) * (DB * 16 * 64);
+    float *xm = reinterpret_cast<float *>(sK1) + wave * 128;
+    if (grp == 1) {
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) xo[(db * 16 + r) * 64 + lane] = oacc[db][r];
+      xm[lane] = m_run;
+      xm[64 + lane] = l_run;
+    }
+    __syncthreads();
+    if (grp == 1) return;
+    const float m1 = xm[lane], l1 = xm[64 + lane];
+    const float mm = fmaxf(m_run, m1);
+    const bool none = mm == kNegInfF;   // neither group saw an unmasked key
+    const float a0 = none ? 0.f : exp2f_(m_run - mm), a1 = none ? 0.f : exp2f_(m1 - mm);
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) oacc[db][r] = oacc[db][r] * a0 + xo[(db * 16 + r) * 64 + lane] * a1;
+    l_run = l_run * a0 + l1 * a1;
+    m_run = mm;
   }
 
   // ---- epilogue: normalise, write O [S, Hq, D] and the natural-log LSE -------
@@ -382,10 +439,30 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
 
 // explicit instantiations: clang otherwise drops some host launch stubs of
 // this template (the bf16 ones), leaving undefined symbols
-template __global__ void attn_fwd_kernel<128, bf16_t>(AttnArgs);
-template __global__ void attn_fwd_kernel<64, bf16_t>(AttnArgs);
-template __global__ void attn_fwd_kernel<128, f16_t>(AttnArgs);
-template __global__ void attn_fwd_kernel<64, f16_t>(AttnArgs);
+template __global__ void attn_fwd_kernel<128, bf16_t, 1>(AttnArgs, int, int);
+template __global__ void attn_fwd_kernel<64, bf16_t, 1>(AttnArgs, int, int);
+template __global__ void attn_fwd_kernel<128, f16_t, 1>(AttnArgs, int, int);
+template __global__ void attn_fwd_kernel<64, f16_t, 1>(AttnArgs, int, int);
+template __global__ void attn_fwd_kernel<128, bf16_t, 2>(AttnArgs, int, int);
+template __global__ void attn_fwd_kernel<64, bf16_t, 2>(AttnArgs, int, int);
+template __global__ void attn_fwd_kernel<128, f16_t, 2>(AttnArgs, int, int);
+template __global__ void attn_fwd_kernel<64, f16_t, 2>(AttnArgs, int, int);
+
+// Items per XCD that the 4-wave launch runs (the rest go to the two-group
+// launch): each XCD takes a contiguous 1/8 of the items on its slots (2
+// four-wave workgroups per CU). When the last round would fill at most half
+// of them -- a half-empty round takes as long as a full one here, a lone
+// workgroup on a CU running no faster -- that round's items run as
+// two-group workgroups (one per CU, each item in about half the time).
+// Items of fewer than 16 tiles are not split.
+int fwd_split_point(int items, int L, int cus) {
+  const int nmax = (items + 7) / 8;
+  const int m = 2 * (cus / 8 > 0 ? cus / 8 : 1);
+  if (L < 16 * kBlock) return nmax;
+  if (nmax <= m / 2) return 0;
+  const int r = nmax % m;
+  return (nmax > m && r > 0 && r <= m / 2) ? nmax - r : nmax;
+}
 
 template <int HD, typename T>
 static void fwd_launch(const AttnArgs &a, hipStream_t st) {
@@ -394,7 +471,11 @@ static void fwd_launch(const AttnArgs &a, hipStream_t st) {
   const int QR = 32 * (4 / HPW);
   const int nqb = (a.S + QR - 1) / QR;
   const int items = a.Hkv * (G / HPW) * nqb;
-  hipLaunchKernelGGL((attn_fwd_kernel<HD, T>), dim3(items), dim3(256), 0, st, a);
+  const int nmax = (items + 7) / 8;
+  const int k1 = fwd_split_point(items, a.L, device_cu_count());
+  if (k1 > 0) hipLaunchKernelGGL((attn_fwd_kernel<HD, T, 1>), dim3(8 * k1), dim3(256), 0, st, a, 0, k1);
+  if (k1 < nmax)
+    hipLaunchKernelGGL((attn_fwd_kernel<HD, T, 2>), dim3(8 * (nmax - k1)), dim3(512), 0, st, a, k1, nmax - k1);
 }
 
 template <int HD>

@@ -148,4 +148,7 @@ void launch_soft_ce_bwd(const void *x, int64_t xs, const void *t, int64_t ts, in
                         bool vec, const float *grad_out, const float *stats, void *g, int64_t gs,
                         hipStream_t stream);
 
+// Compute units of the current device (queried once per device).
+int device_cu_count();
+
 }  // namespace mga

@@ -102,6 +102,24 @@ def test_attention_small_fp16(mga, dev, c):
                    max_abs=F16_MAX_ABS, mean_abs=F16_MEAN_ABS, scaled=True)
 
 
+# Keys of at least 16 tiles and at most one round of items per XCD: the
+# forward runs every item as a two-group workgroup (even and odd tiles of the
+# item's list, merged through LDS). Configs 2 and 4 run the mixed launch (the
+# last round two-group) in test_attention_full_config.
+SPLIT = [
+    dict(n_reg=800, n_anchor=50, draft=4, P=1536, Hq=8, Hkv=2, D=128, pad=11),
+    dict(n_reg=700, n_anchor=60, draft=4, P=1800, Hq=4, Hkv=1, D=64, tail=True),
+]
+
+
+@pytest.mark.parametrize("c", SPLIT)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_attention_two_group_items(mga, dev, c, dtype):
+    seq, q, k, v, kp, vp, do, o, lse = run_case(mga, dev, dtype=dtype, seed=9, **c)
+    tol = dict(max_abs=F16_MAX_ABS, mean_abs=F16_MEAN_ABS, scaled=True) if dtype == torch.float16 else {}
+    compare_oracle(seq, c["P"], q, k, v, kp, vp, do, o, lse, c["D"], grad_start=c["P"], **tol)
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_attention_large_logits(mga, dev, dtype):
     """q, k ~ N(0, 2^2): scaled scores spread over tens of log2 units, so the
