@@ -8,7 +8,10 @@
   pass's calibration copy, a ``kv_copy_rows_kernel`` dispatch that reads and
   writes a known number of bytes (the largest-grid dispatch of that kernel).
   Each kernel's figure is its last dispatch in the pass (the hot-path launch;
-  set-up work such as the prefix fill runs before it).
+  set-up work such as the prefix fill runs before it); for a kernel whose one
+  call is several launches (the forward's 4-wave launch and its two-group
+  tail launch, ``MULTI_LAUNCH``) it is the sum over the last run of
+  consecutive dispatches of that kernel.
 
 * ``mfma``: ``--pmc`` runs of ``bench.py --pmc-pass`` collecting SQ and GRBM
   counters (any number of runs, each its own CSV) turned into per-kernel
@@ -39,11 +42,38 @@ def kernel_base(name: str) -> str:
     return m.group(1).lstrip("_") if m else name[:48]
 
 
+# kernels whose one call may be several consecutive launches
+MULTI_LAUNCH = ("attn_fwd_kernel",)
+
+
+def kernel_label(name: str) -> str:
+    """kernel_base, telling the forward's two-group form (template argument
+    NG = 2, last in its argument list) from the 4-wave one."""
+    k = kernel_base(name)
+    if k == "attn_fwd_kernel":
+        two = re.search(r"Li2EEEv", name) or re.search(r",\s*2>\(", name)
+        return k + (" (two-group)" if two else " (4-wave)")
+    return k
+
+
+def _last_call(seq):
+    """seq: [(kernel, dispatch_id, payload)] in dispatch order -> {kernel:
+    [payloads of its last call]}: the last dispatch, or for MULTI_LAUNCH
+    kernels the last run of consecutive dispatches."""
+    out = {}
+    for i, (k, _, pay) in enumerate(seq):
+        if k in MULTI_LAUNCH and i > 0 and seq[i - 1][0] == k:
+            out[k].append(pay)
+        else:
+            out[k] = [pay]
+    return out
+
+
 def stats_markdown(path: str) -> str:
     rows = list(csv.DictReader(open(path)))
     out = ["| Kernel | Calls | Avg (us) | Share |", "|---|---|---|---|"]
     for r in rows:
-        out.append(f"| {kernel_base(r['Name'])} | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | "
+        out.append(f"| {kernel_label(r['Name'])} | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | "
                    f"{float(r['Percentage']):.2f} % |")
     return "\n".join(out)
 
@@ -69,11 +99,8 @@ def traffic(fetch_csv: str, write_csv: str, calib_read: int, calib_write: int, c
         factor = known / (calib[2] * 1024.0)
         result[f"{counter}_calibration"] = {"known_bytes": known, "counter_KiB": calib[2], "factor": factor}
         # the pass launches each hot-path kernel last (set-up copies come first)
-        last = {}
-        for d in disp:
-            if d is not calib:
-                last[d[0]] = d[2] * 1024.0 * factor
-        scaled[counter] = last
+        calls = _last_call([(d[0], d[3], d[2]) for d in disp if d is not calib])
+        scaled[counter] = {k: sum(v) * 1024.0 * factor for k, v in calls.items()}
     kernels = {}
     for k in sorted(set(scaled["FETCH_SIZE"]) | set(scaled["WRITE_SIZE"])):
         f = scaled["FETCH_SIZE"].get(k, 0.0)
@@ -91,17 +118,29 @@ ATTN_KERNELS = ("attn_fwd_kernel", "attn_bwd_dq_kernel", "attn_bwd_dkdv_kernel")
 
 def counters_by_kernel(paths) -> dict:
     """{kernel: {counter: value}} from the last dispatch of each kernel in
-    every counter CSV (one rocprofv3 --pmc run each)."""
+    every counter CSV (one rocprofv3 --pmc run each). Counters of a
+    MULTI_LAUNCH kernel's launches are summed (cycles and instruction counts
+    add over sequential launches); a derived percentage (MfmaUtil) is
+    weighted by each launch's GRBM_GUI_ACTIVE when the run has it, else
+    averaged."""
     out: dict = {}
     for path in paths:
-        last: dict = {}
+        per: dict = {}
         for r in csv.DictReader(open(path)):
-            k = kernel_base(r["Kernel_Name"])
             d = int(r["Dispatch_Id"])
-            cur = last.setdefault(k, {})
-            cur.setdefault(d, {})[r["Counter_Name"]] = float(r["Counter_Value"])
-        for k, per in last.items():
-            out.setdefault(k, {}).update(per[max(per)])
+            e = per.setdefault(d, {"k": kernel_base(r["Kernel_Name"]), "c": {}})
+            e["c"][r["Counter_Name"]] = float(r["Counter_Value"])
+        calls = _last_call([(e["k"], d, e["c"]) for d, e in sorted(per.items())])
+        for k, runs in calls.items():
+            merged: dict = {}
+            for name in runs[0]:
+                vals = [c.get(name, 0.0) for c in runs]
+                if name == "MfmaUtil":
+                    w = [c.get("GRBM_GUI_ACTIVE", 1.0) for c in runs]
+                    merged[name] = sum(v * x for v, x in zip(vals, w)) / sum(w)
+                else:
+                    merged[name] = sum(vals)
+            out.setdefault(k, {}).update(merged)
     return out
 
 

@@ -37,3 +37,43 @@ def test_kernel_base_names():
     assert rs.kernel_base("_ZN3mga18attn_bwd_dq_kernelILi128EDF16bEEvNS_8AttnArgsE") == "attn_bwd_dq_kernel"
     assert rs.kernel_base("void mga::attn_fwd_kernel<1, 128, float>(mga::AttnArgs)") == "attn_fwd_kernel"
     assert rs.kernel_base("kv_copy_rows_kernel") == "kv_copy_rows_kernel"
+
+
+def test_forward_launches_of_one_call_are_summed(tmp_path):
+    """The forward's 4-wave launch and its two-group tail launch are one call:
+    traffic and counters add over the last run of consecutive forward
+    dispatches; an earlier forward call is not counted, nor is any other
+    kernel's earlier dispatch."""
+    f, w = tmp_path / "f.csv", tmp_path / "w.csv"
+    copy = "kv_copy_rows_kernel"
+    f1 = "_ZN3mga15attn_fwd_kernelILi128EDF16bLi1EEEvNS_8AttnArgsEii"
+    f2 = "_ZN3mga15attn_fwd_kernelILi128EDF16bLi2EEEvNS_8AttnArgsEii"
+    _write(f, "FETCH_SIZE", [(copy, 1000, 512.0), (f1, 10, 7.0), (f2, 5, 9.0), (copy, 80, 40.0),
+                             (f1, 10, 300.0), (f2, 5, 20.0)])
+    _write(w, "WRITE_SIZE", [(copy, 1000, 1024.0), (f1, 10, 1.0), (f2, 5, 1.0), (copy, 80, 80.0),
+                             (f1, 10, 8.0), (f2, 5, 2.0)])
+    r = rs.traffic(str(f), str(w), calib_read=1024 * 1024, calib_write=1024 * 1024, config=2)
+    assert r["kernels"]["attn_fwd_kernel"]["fetch_bytes"] == 2 * 320 * 1024
+    assert r["kernels"]["attn_fwd_kernel"]["write_bytes"] == 10 * 1024
+    assert r["kernels"][copy]["fetch_bytes"] == 80 * 1024
+    c = tmp_path / "c.csv"
+    with open(c, "w", newline="") as fh:
+        wr = csv.DictWriter(fh, fieldnames=FIELDS)
+        wr.writeheader()
+        for d, (name, util, gui, busy) in enumerate([(f1, 40.0, 300.0, 10.0), (f2, 20.0, 100.0, 3.0)]):
+            for cn, v in (("MfmaUtil", util), ("GRBM_GUI_ACTIVE", gui), ("SQ_VALU_MFMA_BUSY_CYCLES", busy)):
+                wr.writerow(dict(Dispatch_Id=d + 1, Grid_Size=1, Kernel_Name=name, Counter_Name=cn,
+                                 Counter_Value=v))
+    got = rs.counters_by_kernel([str(c)])["attn_fwd_kernel"]
+    assert got["GRBM_GUI_ACTIVE"] == 400.0 and got["SQ_VALU_MFMA_BUSY_CYCLES"] == 13.0
+    assert got["MfmaUtil"] == (40.0 * 300.0 + 20.0 * 100.0) / 400.0
+
+
+def test_kernel_labels_tell_the_forward_forms_apart():
+    assert rs.kernel_label("_ZN3mga15attn_fwd_kernelILi128EDF16bLi2EEEvNS_8AttnArgsEii") == \
+        "attn_fwd_kernel (two-group)"
+    assert rs.kernel_label("_ZN3mga15attn_fwd_kernelILi128EDF16bLi1EEEvNS_8AttnArgsEii") == \
+        "attn_fwd_kernel (4-wave)"
+    assert rs.kernel_label("void mga::attn_fwd_kernel<128, __bf16, 2>(mga::AttnArgs, int, int)") == \
+        "attn_fwd_kernel (two-group)"
+    assert rs.kernel_label("_ZN3mga18attn_bwd_dq_kernelILi128EDF16bEEvNS_8AttnArgsE") == "attn_bwd_dq_kernel"
