@@ -109,6 +109,8 @@ def test_attention_small_fp16(mga, dev, c):
 SPLIT = [
     dict(n_reg=800, n_anchor=50, draft=4, P=1536, Hq=8, Hkv=2, D=128, pad=11),
     dict(n_reg=700, n_anchor=60, draft=4, P=1800, Hq=4, Hkv=1, D=64, tail=True),
+    dict(n_reg=600, n_anchor=40, draft=4, P=1700, Hq=8, Hkv=4, D=128),   # G = 2: 64 rows per workgroup
+    dict(n_reg=500, n_anchor=30, draft=4, P=1600, Hq=8, Hkv=1, D=128),   # G = 8: two head slices
 ]
 
 
