@@ -69,8 +69,9 @@ __device__ __forceinline__ f32x16 rows16(const float *t, uint32_t ofs) {
 }
 
 // Global -> LDS staging of a 32 x HD tile (bf16 or fp16) by the two B waves
-// of a group (wl: the loading wave, 0 or 1, wave-uniform): direct loads,
-// completion on vmcnt; rows past rmax repeat row rmax. Addresses are a scalar
+// of a group (wl: the loading wave, 0 or 1, wave-uniform): direct loads as
+// inline asm (dma16), completion on vmcnt waited for by the caller; rows past
+// rmax repeat row rmax. Addresses are a scalar
 // row base plus a 32-bit lane offset (the lane's row term for the source's
 // stride, precomputed, plus its swizzled granule), as in DmaLane.
 template <int HD>
