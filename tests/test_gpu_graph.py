@@ -13,9 +13,15 @@ from gpu_helpers import chunk_layout, qkv
 pytestmark = pytest.mark.gpu
 
 
-def test_attention_step_graph_replays_bit_exact(mga, dev):
+# the last case runs the forward's two launches (4-wave items, then the last
+# round as two-group workgroups); the middle one only two-group workgroups
+CASES = [(300, 25, 4, 200, 8, 2, 128), (800, 50, 4, 1536, 8, 2, 128), (4000, 250, 4, 2048, 32, 8, 128)]
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_attention_step_graph_replays_bit_exact(mga, dev, case):
     ops = mga.ops
-    n_reg, n_anchor, draft, P, Hq, Hkv, D = 300, 25, 4, 200, 8, 2, 128
+    n_reg, n_anchor, draft, P, Hq, Hkv, D = case
     print(f"case n_reg={n_reg} P={P} Hq={Hq} Hkv={Hkv} D={D}", flush=True)
     seq = chunk_layout(n_reg, n_anchor, draft, P, seed=3, pad=11)
     S = len(seq.gate)
