@@ -52,6 +52,7 @@ extern "C" {
 
 #define MGA_BWD_DQ 1        /* mga_attn_bwd: delta = rowsum(o * dout), then dQ */
 #define MGA_BWD_DKDV 2      /* mga_attn_bwd: dK / dV (reads the delta of the dQ pass) */
+#define MGA_BWD_WS_WORDS_PER_ROW 3   /* delta workspace words per (query head, row) */
 
 #define MGA_BLOCK 128       /* BlockMask tile edge, [torch]nn/attention/flex_attention.py:395 */
 
@@ -133,9 +134,11 @@ int mga_attn_fwd(const void *q, int64_t q_sh, int64_t q_ss,
  *   dk, dv [Hkv, L - grad_start, D] for keys j >= grad_start only, summed over
  *   the G query heads of each kv head. With grad_start = P the detached
  *   prefix (collator.py:279-280) gets no gradient and costs no dK/dV work.
- * delta: workspace of Hq * S floats (rowsum(o * dout)), written by the dQ pass
- *   and read by the dK/dV pass. dK/dV are summed over the G query heads inside
- *   the pass, in a fixed order (no other workspace, no atomics).
+ * delta: workspace of MGA_BWD_WS_WORDS_PER_ROW * Hq * S 32-bit words (16-byte
+ *   aligned): the row data of each (query head, row) -- -lse / scale, -delta
+ *   with delta = rowsum(o * dout), and the row's mask threshold -- written by
+ *   the dQ pass and read by the dK/dV pass. dK/dV are summed over the G query
+ *   heads inside the pass, in a fixed order (no other workspace, no atomics).
  * passes: MGA_BWD_DQ | MGA_BWD_DKDV for the full backward. MGA_BWD_DQ alone
  *   serves a caller whose K/V need no gradient; the passes may also be issued
  *   as two calls in stream order (MGA_BWD_DQ first: it writes delta).
@@ -164,8 +167,8 @@ int mga_attn_bwd(const void *q, int64_t q_sh, int64_t q_ss,
  * mga_attn_bwd without the delta workspace argument, for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc). No counterpart in the reference. delta
- * lives in a fixed device array of 2 097 152 floats (8 MiB) that the library
- * holds on every GPU it runs on until the process ends; calls with
+ * lives in a fixed device array of 3 * 2 097 152 words (24 MiB) that the
+ * library holds on every GPU it runs on until the process ends; calls with
  * Hq * S > 2 097 152 are rejected with MGA_ERR_INVALID before any device work.
  * The call itself allocates nothing (no hipMalloc, no library allocation).
  * Every call on a GPU shares that GPU's array and it keeps the last call's

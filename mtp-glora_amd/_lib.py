@@ -24,6 +24,7 @@ DTYPE_F32 = 1
 DTYPE_F16 = 2
 BWD_DQ = 1
 BWD_DKDV = 2
+BWD_WS_WORDS_PER_ROW = 3   # MGA_BWD_WS_WORDS_PER_ROW: delta workspace words per (query head, row)
 
 # name -> argtypes; every function returns int (status) unless listed in _RESTYPES
 _P = ctypes.c_void_p

@@ -93,14 +93,25 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnArgs a) {
   float del = half_row_dot<HD, T>(op, dop, hi);
   del += xor32(del);
   if (!in) del = 0.f;
-  if (in && hi == 0) a.delta[(int64_t)h * a.S + row] = del;
   const float lse = in ? a.lse[(int64_t)h * a.S + row] : kNegInfD;
   // a fully masked row has LSE -inf: it reaches no key (qlim = -1) and its P is 0
   const float lse2 = lse == kNegInfD ? 0.f : lse * kLog2e;
   const float c = a.scale_log2;
   const int qcode = in ? a.code[row] : kCodePad;
   const int qv = query_v(qcode);
-  const int qlim = (qcode == kCodePad || lse == kNegInfD) ? -1 : row + a.P;
+  const bool none = qcode == kCodePad || lse == kNegInfD;
+  const int qlim = none ? -1 : row + a.P;
+  // row data of the dK/dV pass, three planes of Hq * S words: -lse / scale
+  // (0 for a row that sees no key), -delta, and the row's mask threshold
+  // (0: sees no key; 1: regular row, sees the regular keys; 2^31 - 1 - c: mask
+  // row of code c, sees the mask keys of codes >= c). A row past S reads as 0.
+  if (in && hi == 0) {
+    const int64_t plane = (int64_t)a.Hq * a.S, at = (int64_t)h * a.S + row;
+    a.delta[at] = none ? 0.f : -lse * (1.f / a.scale);
+    a.delta[plane + at] = -del;
+    reinterpret_cast<uint32_t *>(a.delta)[2 * plane + at] =
+        none ? 0u : (qcode == kCodeX ? 1u : 0x7fffffffu - (uint32_t)qcode);
+  }
   // keys up to here precede every query of the wave (pad rows are masked by
   // the ordered compare alone: their qv sits above every key)
   const int diag = row - l32 + a.P;

@@ -82,12 +82,13 @@ int check_attn_common(int32_t S, int32_t L, int32_t P, int32_t Hq, int32_t Hkv, 
   return MGA_OK;
 }
 
-// Workspace of mga_attn_bwd_noalloc (delta = rowsum(o * dout) per query head
-// and row): a device array of kNoAllocDeltaFloats floats, one copy on every GPU
-// the library runs on, held until the process ends. Host code reaches it only
-// through the address hipGetSymbolAddress returns for the current device.
-constexpr int64_t kNoAllocDeltaFloats = int64_t(1) << 21;   // 8 MiB: Hq * S <= 2 097 152
-static __device__ __align__(256) float scratch[kNoAllocDeltaFloats];
+// Workspace of mga_attn_bwd_noalloc (the backward's row data: three words per
+// query head and row): a device array of 3 * kNoAllocRows floats, one copy on
+// every GPU the library runs on, held until the process ends. Host code
+// reaches it only through the address hipGetSymbolAddress returns for the
+// current device.
+constexpr int64_t kNoAllocRows = int64_t(1) << 21;   // Hq * S <= 2 097 152 (24 MiB)
+static __device__ __align__(256) float scratch[MGA_BWD_WS_WORDS_PER_ROW * kNoAllocRows];
 
 std::mutex g_scratch_mu;
 constexpr int kMaxDevices = 256;
@@ -239,6 +240,11 @@ int mga_attn_bwd(const void *q, int64_t q_sh, int64_t q_ss, const void *k, int64
   if (!lse || !delta || !code || !kv_num || !kv_idx || !full_kv_num || !full_kv_idx || !q_num ||
       !q_idx || !full_q_num || !full_q_idx)
     return fail(MGA_ERR_INVALID, "mga_attn_bwd: null lse/delta/code/block-mask pointer");
+  // the dK/dV pass addresses the workspace with 32-bit byte offsets
+  if ((int64_t)Hq * S * MGA_BWD_WS_WORDS_PER_ROW * 4 >= (int64_t(1) << 32) - 16)
+    return fail(MGA_ERR_INVALID, "mga_attn_bwd: Hq * S = %lld too large for the delta workspace",
+                (long long)Hq * S);
+  if (!aligned16(delta)) return fail(MGA_ERR_INVALID, "mga_attn_bwd: delta workspace not 16-byte aligned");
   mga::AttnArgs a = {};
   a.q = q; a.q_sh = q_sh; a.q_ss = q_ss;
   a.k = k; a.k_sh = k_sh; a.k_ss = k_ss;
@@ -273,11 +279,11 @@ int mga_attn_bwd_noalloc(const void *q, int64_t q_sh, int64_t q_ss, const void *
                          int32_t Hkv, int32_t head_dim, int32_t dtype, float scale, int32_t passes,
                          void *stream) {
   if (Hq <= 0 || S <= 0) return fail(MGA_ERR_INVALID, "mga_attn_bwd_noalloc: Hq (%d) and S (%d) must be positive", Hq, S);
-  if ((int64_t)Hq * S > kNoAllocDeltaFloats)
+  if ((int64_t)Hq * S > kNoAllocRows)
     return fail(MGA_ERR_INVALID,
                 "mga_attn_bwd_noalloc: Hq * S = %lld exceeds its fixed workspace of %lld (query head, row) "
                 "pairs; use mga_attn_bwd with a caller-allocated delta",
-                (long long)Hq * S, (long long)kNoAllocDeltaFloats);
+                (long long)Hq * S, (long long)kNoAllocRows);
   float *delta = nullptr;
   int rc = scratch_for_current_device(&delta);
   if (rc != MGA_OK) return rc;

@@ -27,8 +27,9 @@
 // (a row's first unmasked scores, or a score more than 20 log2 units above m)
 // the step takes the slow path: m moves to the exact running max, O and the
 // row sum are rescaled and the probabilities recomputed from the scores still
-// held in registers. Row sums are taken from the rounded probabilities the O
-// update multiplies (v_dot2), so the normalisation matches the weights used.
+// held in registers. Row sums add the fp32 probabilities, before they are
+// rounded to the operand type for the O update, as the reference's kernel
+// does ([torch]_inductor/kernel/flex/templates/common.py.jinja:101, 114).
 // Masking runs only on partial tiles: one ordered compare per score (see
 // key_w; it also masks pad rows), plus the causal bound only on the steps
 // whose keys reach past the wave's first query.
@@ -252,16 +253,16 @@ __global__ __launch_bounds__(256 * NG, 2) void attn_fwd_kernel(AttnArgs a, int k
             x0 += d;
             x1 += d;
           }
-          const uint32_t w = cvt2<E>(exp2f_(x0), exp2f_(x1));
-          wv[q] = (int)w;
-          ps = add_pair<E>(w, ps);
+          const float e0 = exp2f_(x0), e1 = exp2f_(x1);
+          wv[q] = (int)cvt2<E>(e0, e1);
+          ps += e0 + e1;
         }
         pb[2 * kb + u] = __builtin_bit_cast(bf16x8, wv);
       }
     return ps;
   };
   // the interleave of a fused region: K reads, MFMAs and the VALU work of
-  // shift + probs (32 fma + 32 exp2 + 16 cvt + 16 dot2 per step)
+  // shift + probs (32 fma + 32 exp2 + 16 cvt + 32 adds per step)
   auto interleave = [&]() {
     constexpr int kValuPer = 96 / (KS * kStepBlocks);
 #pragma unroll

@@ -181,8 +181,9 @@ def attn_fwd(q, k, v, code, bm: dict, P: int, scale: float):
 
 def bwd_buffers(q, k, grad_start: int) -> dict:
     """Output and workspace buffers of ``attn_bwd``: dq [1, S, Hq, D], dk/dv
-    [1, L - grad_start, Hkv, D] (None when grad_start == L) and delta
-    [Hq * S] fp32."""
+    [1, L - grad_start, Hkv, D] (None when grad_start == L) and delta, the
+    backward's row-data workspace of ``BWD_WS_WORDS_PER_ROW * Hq * S`` 32-bit
+    words (fp32 storage)."""
     _, Hq, S, D = q.shape
     _, Hkv, L, _ = k.shape
     dev, dt = q.device, q.dtype
@@ -190,7 +191,7 @@ def bwd_buffers(q, k, grad_start: int) -> dict:
     return dict(dq=torch.empty(1, S, Hq, D, dtype=dt, device=dev),
                 dk=torch.empty(1, Lg, Hkv, D, dtype=dt, device=dev) if Lg > 0 else None,
                 dv=torch.empty(1, Lg, Hkv, D, dtype=dt, device=dev) if Lg > 0 else None,
-                delta=torch.empty(Hq * S, dtype=torch.float32, device=dev))
+                delta=torch.empty(_lib.BWD_WS_WORDS_PER_ROW * Hq * S, dtype=torch.float32, device=dev))
 
 
 def attn_bwd(q, k, v, o, lse, dout, code, bm: dict, P: int, scale: float, grad_start: int,
@@ -223,7 +224,7 @@ def attn_bwd(q, k, v, o, lse, dout, code, bm: dict, P: int, scale: float, grad_s
         d3 = d3.contiguous()
     b = buffers if buffers is not None else bwd_buffers(q, k, grad_start)
     dq, dk, dv, delta = b["dq"], b["dk"], b["dv"], b["delta"]
-    if dq.shape != (1, S, Hq, D) or delta.numel() != Hq * S:
+    if dq.shape != (1, S, Hq, D) or delta.numel() != _lib.BWD_WS_WORDS_PER_ROW * Hq * S:
         raise ValueError("backward buffers do not match the operands")
     dk_ptr = dk.data_ptr() if dk is not None else None
     dv_ptr = dv.data_ptr() if dv is not None else None

@@ -110,10 +110,15 @@ def round_to(dtype):
 
 def rounding_model_grad_errors(q, k, v, do, allowed, scale, grad_start, rnd):
     """Error against float64 of attention gradients computed with only the
-    reference's 16-bit rounding points (its compiled flex kernels cast P to the
-    operand dtype before dV = P^T dO, and dS before dQ and dK), everything else
-    in float64. Returns {name: (max-abs, mean-abs)} for dq, dk, dv: the error
-    floor of any implementation with those rounding points on these inputs."""
+    reference's 16-bit rounding points, everything else in float64: the
+    forward's output is stored in the operand dtype and delta = rowsum(out *
+    grad_out) is formed from that stored output
+    ([torch]_inductor/kernel/flex/flex_attention.py:750-751), and the compiled
+    backward casts P to the operand dtype before dV = P^T dO and dS before dQ
+    and dK (flex_backwards.py.jinja:570-618) and stores dQ, dK and dV in the
+    operand dtype (:177, 273, 287). Returns {name: (max-abs, mean-abs)} for dq,
+    dk, dv: the error floor of any implementation with those rounding points on
+    these inputs."""
     o, lse = mo.attention_fwd(q, k, v, allowed, scale)
     exact = mo.attention_bwd(q, k, v, o, lse, do, allowed, scale, grad_start=grad_start)
     Hq, S, D = q.shape
@@ -128,9 +133,9 @@ def rounding_model_grad_errors(q, k, v, do, allowed, scale, grad_start, rnd):
         rowok = np.isfinite(lse[h])
         p = np.where(allowed & rowok[:, None], np.exp(s - np.where(rowok, lse[h], 0.0)[:, None]), 0.0)
         dv[g] += rnd(p).T @ do[h]
-        ds = rnd(p * (do[h] @ v[g].T - (o[h] * do[h]).sum(axis=1)[:, None]))
+        ds = rnd(p * (do[h] @ v[g].T - (rnd(o[h]) * do[h]).sum(axis=1)[:, None]))
         dq[h] = scale * (ds @ k[g])
         dk[g] += scale * (ds.T @ q[h])
-    got = (dq, dk[:, grad_start:], dv[:, grad_start:])
+    got = (rnd(dq), rnd(dk[:, grad_start:]), rnd(dv[:, grad_start:]))
     return {n: (float(np.abs(a - b).max()), float(np.abs(a - b).mean()))
             for n, a, b in zip(("dq", "dk", "dv"), got, exact)}

@@ -132,10 +132,13 @@ def test_attention_large_logits(mga, dev, dtype):
     outputs near 6, where one bf16 rounding is 1.6e-2). Gradients grow to |dq| ~ 13 here and dS to tens
     of units, so the 16-bit roundings of P and dS alone (the reference's
     rounding points) cost more than the O(1)-scale bounds: each gradient must
-    stay within 3x the max- and mean-abs error of that rounding model
-    (rounding_model_grad_errors) on the same inputs; the factor covers this
-    kernel's further roundings (outputs, the LSE summed from rounded
-    probabilities, delta from the stored output)."""
+    stay within 2x the max- and mean-abs error of that rounding model
+    (rounding_model_grad_errors: the reference's cast points, delta from the
+    stored output and the 16-bit gradient stores included) on the same
+    inputs; the factor covers fp32 sums in another order and probabilities
+    that round the other way. dS is formed from the fp32 P in both passes and
+    the forward's row sums from the fp32 probabilities, as the reference
+    does."""
     c = dict(n_reg=320, n_anchor=24, draft=4, P=192, Hq=4, Hkv=2, D=128)
     seq, q, k, v, kp, vp, do, o, lse = run_case(mga, dev, dtype=dtype, seed=11, std=2.0, **c)
     P, D = c["P"], c["D"]
@@ -157,8 +160,10 @@ def test_attention_large_logits(mga, dev, dtype):
     model = rounding_model_grad_errors(qn, kn, vn, don, allowed, D ** -0.5, P, round_to(dtype))
     for name, got, ref in (("dq", q.grad, dqn), ("dk", k.grad, dkn), ("dv", v.grad, dvn)):
         mx, mn = model[name]
-        print(f"  {name} rounding model: max-abs {mx:.3e} mean-abs {mn:.3e}", flush=True)
-        check(name, f64(got)[0], ref, max_abs=3 * mx, mean_abs=3 * mn)
+        err = np.abs(f64(got)[0] - ref)
+        print(f"  {name} rounding model: max-abs {mx:.3e} mean-abs {mn:.3e}; kernel / model: "
+              f"max {err.max() / mx:.2f} mean {err.mean() / mn:.2f}", flush=True)
+        check(name, f64(got)[0], ref, max_abs=2 * mx, mean_abs=2 * mn)
 
 
 @pytest.mark.parametrize("c", SMALL)
