@@ -119,6 +119,9 @@ class StreamingKVCache:
 
     @staticmethod
     def _in_place(t: torch.Tensor, buf: torch.Tensor, P: int) -> bool:
+        # a full buffer has no row P: the append then raises its capacity error
+        if P >= buf.shape[1]:
+            return False
         return (t.data_ptr() == buf[:, P].data_ptr() and t.stride()[1:] == buf.stride()
                 and t.shape[1] == buf.shape[0])
 

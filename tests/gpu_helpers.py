@@ -139,3 +139,61 @@ def rounding_model_grad_errors(q, k, v, do, allowed, scale, grad_start, rnd):
     got = (rnd(dq), rnd(dk[:, grad_start:]), rnd(dv[:, grad_start:]))
     return {n: (float(np.abs(a - b).max()), float(np.abs(a - b).mean()))
             for n, a, b in zip(("dq", "dk", "dv"), got, exact)}
+
+
+def torch_rounding_model_grads(q, kfull, vfull, allowed, scale, do, grad_start, dtype):
+    """rounding_model_grad_errors' gradients computed on the GPU in fp32 (for the
+    full-size stream shapes the float64 oracle is too slow for): the
+    reference's 16-bit rounding points -- the stored output that delta is
+    formed from, P before dV = P^T dO, dS before dQ and dK, and the 16-bit
+    gradient stores -- and fp32 everywhere else, one query head at a time.
+    Returns dq [Hq, S, D], dk, dv [Hkv, L - grad_start, D] as fp32 tensors."""
+    rnd = lambda t: t.to(dtype).float()
+    Hq, S, D = q.shape[1], q.shape[2], q.shape[3]
+    Hkv, L = kfull.shape[1], kfull.shape[2]
+    G = Hq // Hkv
+    m = torch.as_tensor(allowed, device=q.device)
+    rowok = m.any(dim=1)
+    dq = torch.empty(Hq, S, D, device=q.device)
+    dk = torch.zeros(Hkv, L, D, device=q.device)
+    dv = torch.zeros(Hkv, L, D, device=q.device)
+    for h in range(Hq):
+        g = h // G
+        qh, kh, vh = q[0, h].float(), kfull[0, g].float(), vfull[0, g].float()
+        doh = do[0, :, h].float()
+        s = ((qh @ kh.T) * scale).masked_fill(~m, float("-inf"))
+        lse = torch.where(rowok, torch.logsumexp(s, dim=1), torch.zeros_like(s[:, 0]))
+        p = torch.where(m & rowok[:, None], torch.exp(s - lse[:, None]), torch.zeros_like(s))
+        del s
+        o = rnd(p @ vh)
+        dv[g] += rnd(p).T @ doh
+        ds = rnd(p * (doh @ vh.T - (o * doh).sum(dim=1)[:, None]))
+        del p
+        dq[h] = scale * (ds @ kh)
+        dk[g] += scale * (ds.T @ qh)
+        del ds
+    return rnd(dq), rnd(dk[:, grad_start:]), rnd(dv[:, grad_start:])
+
+
+def check_grad(name, got, ref, model, k=2.0, max_abs=MAX_ABS, mean_abs=MEAN_ABS):
+    """A gradient against the exact reference: within the absolute bound
+    (max-abs max_abs, mean-abs mean_abs), or within k times the max- and
+    mean-abs error of the reference's rounding model on the same inputs
+    (model: its gradient, or its (max-abs, mean-abs) errors), whichever is
+    larger. The model measures what the 16-bit rounding points alone cost: with
+    |dV| near 7, one bf16 rounding is 1.6e-2, so an absolute 2e-2 is then below
+    what the reference's own flex path can meet."""
+    g = np.asarray(got, np.float64)
+    r = np.asarray(ref, np.float64)
+    if isinstance(model, tuple):
+        mmx, mmn = model
+    else:
+        me = np.abs(np.asarray(model, np.float64) - r)
+        mmx, mmn = float(me.max()), float(me.mean())
+    err = np.abs(g - r)
+    mx, mn = float(err.max()), float(err.mean())
+    bmx, bmn = max(max_abs, k * mmx), max(mean_abs, k * mmn)
+    print(f"  {name}: max-abs {mx:.3e} mean-abs {mn:.3e}; rounding model max-abs {mmx:.3e} "
+          f"mean-abs {mmn:.3e}; bounds {bmx:.3e} / {bmn:.3e} (k = {k})", flush=True)
+    assert np.isfinite(g).all(), f"{name} has non-finite values"
+    assert mx <= bmx and mn <= bmn, f"{name}: max-abs {mx:.3e} mean-abs {mn:.3e} > bounds {bmx:.3e} / {bmn:.3e}"

@@ -79,3 +79,58 @@ def test_attention_step_graph_replays_bit_exact(mga, dev, case):
         for i, (got, want) in enumerate(zip(out, eager)):
             assert torch.equal(got, want), f"replay {rep}: output {i} differs from the eager run"
         print(f"  replay {rep}: {len(out)} outputs bit-exact", flush=True)
+
+
+@pytest.mark.parametrize("split_passes", [False, True])
+def test_noalloc_backward_graph_replays_bit_exact(mga, dev, split_passes):
+    """mga_attn_bwd_noalloc captured in a HIP graph, both passes in one call
+    and as two calls, replayed three times against the eager allocating
+    mga_attn_bwd, bit for bit. Between replays an eager no-alloc call on other
+    inputs overwrites the per-GPU workspace the graph's calls share, and the
+    outputs are scribbled over. The first no-alloc call of a test process is
+    this test's capture, so the per-device lookup of the workspace runs under
+    capture."""
+    ops, lib = mga.ops, mga._lib
+    print(f"noalloc graph split={split_passes}", flush=True)
+
+    def inputs(n_reg, n_anchor, P, Hq, Hkv, D, seed):
+        seq = chunk_layout(n_reg, n_anchor, 4, P, seed=seed, pad=9)
+        S = len(seq.gate)
+        q, k, v, kp, vp, do = qkv(S, P, Hq, Hkv, D, torch.bfloat16, dev, seed=seed)
+        bm = mga.build_mtp_block_mask(torch.tensor(seq.gate, device=dev)[None], P)
+        kf, vf = torch.cat([kp, k], dim=2), torch.cat([vp, v], dim=2)
+        bmt = bm.kernel_tensors()
+        o, lse = ops.attn_fwd(q, kf, vf, bm.mtp_code, bmt, P, D ** -0.5)
+        return q, kf, vf, o, lse, do, bm.mtp_code, bmt, P, D
+
+    q, kf, vf, o, lse, do, code, bmt, P, D = inputs(800, 50, 1536, 8, 2, 128, 4)
+    other = inputs(300, 20, 256, 4, 2, 128, 5)
+    scale = D ** -0.5
+    want = ops.attn_bwd(q, kf, vf, o, lse, do, code, bmt, P, scale, P)
+    bufs = ops.bwd_buffers(q, kf, P)
+    torch.cuda.synchronize()
+
+    def work():
+        if split_passes:
+            ops.attn_bwd(q, kf, vf, o, lse, do, code, bmt, P, scale, P, passes=lib.BWD_DQ, buffers=bufs,
+                         no_alloc=True)
+            ops.attn_bwd(q, kf, vf, o, lse, do, code, bmt, P, scale, P, passes=lib.BWD_DKDV, buffers=bufs,
+                         no_alloc=True)
+        else:
+            ops.attn_bwd(q, kf, vf, o, lse, do, code, bmt, P, scale, P, buffers=bufs, no_alloc=True)
+
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        work()
+    got = (bufs["dq"].transpose(1, 2), bufs["dk"].transpose(1, 2), bufs["dv"].transpose(1, 2))
+    for rep in range(3):
+        oq, okf, ovf, oo, olse, odo, ocode, obmt, oP, oD = other
+        ops.attn_bwd(oq, okf, ovf, oo, olse, odo, ocode, obmt, oP, oD ** -0.5, oP, no_alloc=True)
+        for t in (bufs["dq"], bufs["dk"], bufs["dv"]):
+            t.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for name, g, w in zip(("dq", "dk", "dv"), got, want):
+            assert torch.equal(g, w), f"replay {rep}: {name} differs from the eager allocating call"
+        print(f"  replay {rep}: dq, dk, dv bit-exact", flush=True)

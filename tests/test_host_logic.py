@@ -95,3 +95,17 @@ def test_manager_api_surface(mga):
     m.reset_cache()
     assert m.past_seen_tokens == 0
     assert m.extract_regular_kv_cache_for_next_chunk({"input_ids": torch.zeros(1, 4)}, None) is None
+
+
+def test_cache_raise_paths_before_allocation(mga):
+    """Raise paths that need no device memory: a carry-over before any update,
+    an update of a cache that does not know its layer count, a crop below an
+    empty prefix."""
+    c = mga.StreamingKVCache(capacity=16, num_layers=2)
+    with pytest.raises(RuntimeError, match="commit_regular before any update"):
+        c.commit_regular(torch.zeros(4, dtype=torch.int32), 0)
+    k = torch.zeros(1, 2, 4, 64)
+    with pytest.raises(RuntimeError, match="needs num_layers"):
+        mga.StreamingKVCache(capacity=16).update(k, k, 0)
+    with pytest.raises(ValueError, match="negative"):
+        c.crop(-1)
