@@ -22,10 +22,15 @@ detached prefix: Hq*D*[4(A_pre+A_cur) + 6 A_pre + 10 A_cur]. Per-kernel
 durations (HIP events on the launch stream) give the roofline fractions.
 
 ``cpu_baseline``: the reference's CPU path (torch flex_attention eager -- the
-dense math path -- fwd + autograd bwd on the restated MTP mask_mod) on one
-KV-head group (4 query heads, full S and P+S), median of timed runs; beside
-it, ``compiled_fwd_only``: torch.compile(flex_attention) forward on the same
-sample, which on the CPU serves inference only (no LSE, no backward).
+dense math path -- fwd + autograd bwd on the restated MTP mask_mod) over the
+whole layer-chunk, one KV-head group (4 query heads, full S and P+S) after
+another; beside it, ``compiled_fwd_only``: torch.compile(flex_attention)
+forward on the first group, which on the CPU serves inference only (no LSE,
+no backward).
+
+``north_star``, ``config3_stream`` and ``config5_step``: the north-star point
+(config 3's last chunk as one layer-chunk step), the whole config-3 stream (36
+layers x 8 chunks) and the config-5 step, timed in the same run.
 """
 from __future__ import annotations
 
@@ -367,9 +372,13 @@ def cpu_compiled_fwd(torch, fr, q, k, v, bm, scale: float, reps: int) -> dict:
     return dict(seconds=statistics.median(times), compile_s=compile_s)
 
 
-def cpu_baseline(cfg: dict, gate_cpu, reps: int, heads: int, compiled: bool) -> dict:
-    """The reference's CPU attention path on one KV-head group (and, with
-    ``compiled``, the compiled inference-only forward on the same inputs)."""
+def cpu_baseline(cfg: dict, gate_cpu, reps: int, heads: int, compiled: bool, groups: int = 1) -> dict:
+    """The reference's CPU attention path over ``groups`` KV-head groups of
+    ``heads`` query heads each, one after another (the eager dense path
+    materialises fp32 [heads, S, P+S] scores, so one group at a time), each
+    with its own inputs: ``reps`` passes over the groups after a warm-up call,
+    ``seconds`` = the median pass's total. With ``compiled``, the compiled
+    inference-only forward on the first group's inputs."""
     import torch
     from oracle import flex_ref as fr
     threads = min(os.cpu_count() or 1, 16)
@@ -380,20 +389,26 @@ def cpu_baseline(cfg: dict, gate_cpu, reps: int, heads: int, compiled: bool) -> 
     t0 = time.perf_counter()
     bm = fr.reference_block_mask(gate_cpu, P)
     mask_s = time.perf_counter() - t0
-    g = torch.Generator().manual_seed(SEED)
-    q = (torch.randn(1, heads, S, D, generator=g) * 0.5).bfloat16()
-    k = (torch.randn(1, 1, L, D, generator=g) * 0.5).bfloat16()
-    v = (torch.randn(1, 1, L, D, generator=g) * 0.5).bfloat16()
-    do = torch.randn(1, heads, S, D, generator=g).bfloat16()
+    data = []
+    for grp in range(groups):
+        g = torch.Generator().manual_seed(SEED + 100 * grp)
+        data.append(((torch.randn(1, heads, S, D, generator=g) * 0.5).bfloat16(),
+                     (torch.randn(1, 1, L, D, generator=g) * 0.5).bfloat16(),
+                     (torch.randn(1, 1, L, D, generator=g) * 0.5).bfloat16(),
+                     torch.randn(1, heads, S, D, generator=g).bfloat16()))
+    q, k, v, do = data[0]
     import warnings
     with warnings.catch_warnings():
         warnings.simplefilter("ignore")
         fr.reference_attention(q, k, v, bm, D ** -0.5, do=do)          # warm-up
         times = []
         for _ in range(reps):
-            t0 = time.perf_counter()
-            fr.reference_attention(q, k, v, bm, D ** -0.5, do=do)
-            times.append(time.perf_counter() - t0)
+            total = 0.0
+            for qg, kg, vg, dog in data:
+                t0 = time.perf_counter()
+                fr.reference_attention(qg, kg, vg, bm, D ** -0.5, do=dog)
+                total += time.perf_counter() - t0
+            times.append(total)
     comp = None
     if compiled:
         try:
@@ -434,19 +449,22 @@ def load_mfma(path: str) -> dict:
     return out
 
 
-def north_star_phase(torch, mga, syn, steps: int, warmup: int) -> dict:
-    """The north-star point: one Qwen3-8B layer-chunk of 4096 regular rows plus
-    512 anchors x 4 mask rows (S = 6144) against a 28 672-token cached prefix
-    (config 3's last chunk), timed as the main step is: block mask, staging
-    append, attention forward and backward, regular-row commit."""
+def layer_step_phase(torch, mga, syn, geo: dict, steps: int, warmup: int, seed: int) -> dict:
+    """One layer-chunk step at geometry ``geo`` (a CONFIGS entry), timed as the
+    main step is: block mask, staging append, attention forward and backward,
+    regular-row commit, the cache cropped back to the same prefix."""
     dev = torch.device("cuda:0")
-    Hq, Hkv, D, P, n_reg, n_anchor, draft = 32, 8, 128, 28672, 4096, 512, 4
-    anchors = syn.sample_anchors(n_reg, n_anchor, SEED + 7)
-    chunk0 = syn.mtp_chunk(n_reg, anchors, draft, pos0=P, device=dev, seed=SEED + 7)
+    Hq, Hkv, D, P = geo["Hq"], geo["Hkv"], geo["D"], geo["P"]
+    n_reg, n_anchor, draft = geo["n_reg"], geo["n_anchor"], geo["draft"]
+    if geo["every"]:
+        anchors = syn.every_kth_anchor(n_reg, geo["every"], n_anchor)
+    else:
+        anchors = syn.sample_anchors(n_reg, n_anchor, seed)
+    chunk0 = syn.mtp_chunk(n_reg, anchors, draft, pos0=P, device=dev, seed=seed)
     S = chunk0["gate_mask"].shape[1]
     L = P + S
     scale = D ** -0.5
-    gens = [torch.Generator(device=dev).manual_seed(SEED + 70 + i) for i in range(6)]
+    gens = [torch.Generator(device=dev).manual_seed(seed * 10 + i) for i in range(6)]
     rnd = lambda shape, g, sd: (torch.randn(*shape, generator=g, device=dev) * sd).bfloat16()
     q = rnd((1, S, Hq, D), gens[0], 0.5).transpose(1, 2).requires_grad_()
     k = rnd((1, S, Hkv, D), gens[1], 0.5).transpose(1, 2).requires_grad_()
@@ -482,11 +500,23 @@ def north_star_phase(torch, mga, syn, steps: int, warmup: int) -> dict:
     a_pre, a_cur = tile_areas(bm, S, L, P)
     fl = Hq * D * (4 * (a_pre + a_cur) + 6 * a_pre + 10 * a_cur)
     tf = fl / (ms * 1e-3) / 1e12
-    return {"workload": "north-star point: Qwen3-8B layer-chunk, 4096 regular + 512x4 mask rows vs a "
-                        "28672-token prefix (config 3, last chunk)",
-            "chunk_rows": S, "prefix": P, "credited_gflop": round(fl / 1e9, 1), "ms_per_step": round(ms, 4),
-            "tflops": round(tf, 2), "frac": round(tf / PEAK_MFMA_BF16_TFLOPS, 4), "steps": steps,
-            "target_frac": 0.5}
+    return {"chunk_rows": S, "prefix": P, "credited_gflop": round(fl / 1e9, 1), "ms_per_step": round(ms, 4),
+            "tflops": round(tf, 2), "frac": round(tf / PEAK_MFMA_BF16_TFLOPS, 4), "steps": steps}
+
+
+# config 3's last chunk: the north-star point
+NORTH_STAR = dict(Hq=32, Hkv=8, D=128, P=28672, n_reg=4096, n_anchor=512, draft=4, every=None)
+
+
+def north_star_phase(torch, mga, syn, steps: int, warmup: int) -> dict:
+    """The north-star point: one Qwen3-8B layer-chunk of 4096 regular rows plus
+    512 anchors x 4 mask rows (S = 6144) against a 28 672-token cached prefix
+    (config 3's last chunk)."""
+    out = {"workload": "north-star point: Qwen3-8B layer-chunk, 4096 regular + 512x4 mask rows vs a "
+                       "28672-token prefix (config 3, last chunk)"}
+    out.update(layer_step_phase(torch, mga, syn, NORTH_STAR, steps, warmup, SEED + 7))
+    out["target_frac"] = 0.5
+    return out
 
 
 def load_traffic(path: str, config: int):
@@ -566,7 +596,7 @@ def pmc_pass(torch, mga, libc, q, k, v, do, kp, cache, chunk0, P, S, R, Hkv, D, 
     return 0
 
 
-def stream_bench(torch, mga, syn, config: int, cfg: dict, cpu_reps: int = 0) -> int:
+def stream_measure(torch, mga, syn, cfg: dict) -> dict:
     """Time one whole chunk stream (all layers, all chunks) through the
     drop-in API after a one-chunk warm-up; credited FLOPs per chunk from that
     chunk's block mask, times the layer count."""
@@ -629,6 +659,17 @@ def stream_bench(torch, mga, syn, config: int, cfg: dict, cpu_reps: int = 0) -> 
             append_bytes += nl * 2 * R * Hkv * D * 2 * 2
         P += R
     tflops = credited / seconds / 1e12
+    return dict(chunks=chunks, credited=credited, seconds=seconds, host_s=host_s, append_bytes=append_bytes,
+                final_prefix=P, tflops=tflops)
+
+
+def stream_bench(torch, mga, syn, config: int, cfg: dict, cpu_reps: int = 0) -> int:
+    """The stream of ``cfg`` as the bench line (``--config 3`` / ``4``), with
+    the CPU baseline sampled at three of its chunks."""
+    Hq, Hkv, D, nl = cfg["Hq"], cfg["Hkv"], cfg["D"], cfg["layers"]
+    m = stream_measure(torch, mga, syn, cfg)
+    chunks, credited, seconds, tflops, P = m["chunks"], m["credited"], m["seconds"], m["tflops"], m["final_prefix"]
+    host_s, append_bytes = m["host_s"], m["append_bytes"]
     cpu = None
     if cpu_reps > 0:
         # the reference's CPU path at the stream's first, middle and last chunk
@@ -678,8 +719,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", type=int, default=2, choices=sorted(set(CONFIGS) | set(STREAMS)))
-    ap.add_argument("--cpu-reps", type=int, default=3, help="timed runs of the CPU baseline (0 = skip)")
-    ap.add_argument("--cpu-heads", type=int, default=4, help="query heads in the CPU sample (one KV group)")
+    ap.add_argument("--cpu-reps", type=int, default=1,
+                    help="timed passes of the CPU baseline over the layer's KV-head groups (0 = skip)")
     ap.add_argument("--cpu-compiled", type=int, default=1,
                     help="also time the compiled (inference-only) CPU forward on the same sample (0 = skip)")
     ap.add_argument("--phase-iters", type=int, default=20)
@@ -692,6 +733,8 @@ def main() -> int:
                     help="counter summary (rocprof_summary.py mfma) that fills roofline.mfma_busy")
     ap.add_argument("--north-star-steps", type=int, default=10,
                     help="timed steps of the north-star point (0 = skip)")
+    ap.add_argument("--extra", type=int, default=1,
+                    help="also time the config-3 stream (36 layers x 8 chunks) and the config-5 step (0 = skip)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -867,31 +910,42 @@ def main() -> int:
     }
     if args.north_star_steps > 0:
         out["north_star"] = north_star_phase(torch, mga, syn, args.north_star_steps, 3)
+    if args.extra and args.config == 2:
+        # the other workloads BASELINE.md quotes, measured in the same run
+        st = STREAMS[3]
+        m = stream_measure(torch, mga, syn, st)
+        out["config3_stream"] = {"workload": st["workload"], "credited_tflop": round(m["credited"] / 1e12, 2),
+                                 "seconds": round(m["seconds"], 4), "tflops": round(m["tflops"], 2),
+                                 "frac": round(m["tflops"] / PEAK_MFMA_BF16_TFLOPS, 4),
+                                 "append_bytes": m["append_bytes"], "final_prefix": m["final_prefix"]}
+        del m
+        c5 = {"workload": CONFIGS[5]["workload"]}
+        c5.update(layer_step_phase(torch, mga, syn, CONFIGS[5], 10, 3, SEED))
+        out["config5_step"] = c5
 
     if args.cpu_reps > 0:
-        cb = cpu_baseline(cfg, chunk0["gate_mask"].cpu(), args.cpu_reps, args.cpu_heads, args.cpu_compiled)
-        frac = args.cpu_heads / Hq
-        cpu_tflops = fl_total * frac / cb["seconds"] / 1e12
+        G = Hq // Hkv
+        cb = cpu_baseline(cfg, chunk0["gate_mask"].cpu(), args.cpu_reps, G, args.cpu_compiled, groups=Hkv)
+        cpu_tflops = fl_total / cb["seconds"] / 1e12
         out["cpu_baseline"] = {
             "value": round(cpu_tflops, 4), "unit": "TFLOP/s", "cores": cb["threads"], "kind": "port",
-            "sample": (f"torch flex_attention eager (dense math path) fwd+bwd on CPU with the restated "
-                       f"MTP mask_mod: {args.cpu_heads} query heads of one KV head at the full "
-                       f"S={S}, P+S={L}; median of {args.cpu_reps} runs after a warm-up; value "
-                       f"extrapolated from this one of {Hq // args.cpu_heads} KV-head groups (credited "
-                       f"FLOPs of the sample = {args.cpu_heads}/{Hq} of the layer's)"),
-            "extrapolated": f"x{Hq // args.cpu_heads} (one KV-head group timed)",
-            "seconds": round(cb["seconds"], 3), "mask_build_s": round(cb["mask_build_s"], 3),
+            "sample": (f"the whole layer-chunk: torch flex_attention eager (dense math path) fwd+bwd on CPU "
+                       f"with the restated MTP mask_mod, all {Hkv} KV-head groups of {G} query heads at the "
+                       f"full S={S}, P+S={L}, one group after another (each its own inputs), summed; "
+                       f"median of {args.cpu_reps} pass(es) after a warm-up call; no extrapolation"),
+            "seconds": round(cb["seconds"], 3), "group_seconds": [round(t / Hkv, 3) for t in cb["times"]],
+            "mask_build_s": round(cb["mask_build_s"], 3),
             "cpu_count": cb["cpu_count"], "cpu_model": cb["cpu_model"],
         }
         comp = cb["compiled"]
         if comp is not None:
             entry = {"label": ("inference-only: torch.compile(flex_attention) forward on the CPU, no LSE "
-                               "and no backward (Inductor's CPU flex kernel refuses both), same inputs "
-                               "and block mask, one KV-head group extrapolated like the value")}
+                               "and no backward (Inductor's CPU flex kernel refuses both), the first "
+                               f"KV-head group's inputs and block mask, extrapolated x{Hkv} to the layer")}
             if "error" in comp:
                 entry["error"] = comp["error"]
             else:
-                entry.update({"value": round(fl_fwd * frac / comp["seconds"] / 1e12, 4), "unit": "TFLOP/s",
+                entry.update({"value": round(fl_fwd / Hkv / comp["seconds"] / 1e12, 4), "unit": "TFLOP/s",
                               "seconds": round(comp["seconds"], 4), "compile_s": round(comp["compile_s"], 1),
                               "gpu_fwd_tflops": out["attention"]["fwd_tflops"]})
             out["cpu_baseline"]["compiled_fwd_only"] = entry
