@@ -265,8 +265,10 @@ int mga_qk_norm_rope_bwd(const void *q, int64_t q_token_stride, int64_t q_head_s
                          void *dk, int64_t dk_token_stride, int64_t dk_head_stride, void *stream);
 
 /*
- * Gated LoRA linear layer, bf16 (GatedLoRALinear.forward,
- * mtp_glora/models/layers/gated_lora.py:51-53):
+ * Gated LoRA linear layer (GatedLoRALinear.forward,
+ * mtp_glora/models/layers/gated_lora.py:51-53), operands of one dtype code
+ * (MGA_DTYPE_BF16, MGA_DTYPE_F16 or MGA_DTYPE_F32, the reference's model
+ * dtypes, args.py:15):
  *   y = x W^T + scaling * B(A(dropout(x))) * gate,
  * computed as y = T(x W^T + T(t B^T)) (the base GEMM accumulates onto the
  * rounded LoRA term), for x [S, K] (row stride x_rs), W [N, K], A =
@@ -274,15 +276,18 @@ int mga_qk_norm_rope_bwd(const void *q, int64_t q_token_stride, int64_t q_head_s
  * B = lora_B.weight [N, rank], gate [S] fp32 (NULL = 1; the reference's
  * clamped gate mask). Writes y [S, N] and, for the backward, t [S, rpad]
  * (rpad = rank rounded up to 32; t = T(T(scaling * T(h A^T)) * gate), T =
- * bf16 rounding, h = dropout(x)) and, when dropout_p > 0 and h is not
- * NULL, h [S, K] (NULL: h is not kept and the backward draws the mask again
- * from x, which needs K a multiple of 128).
+ * rounding to the dtype, h = dropout(x)) and, when dropout_p > 0 and h is not
+ * NULL, h [S, K] (NULL, bf16 only: h is not kept and the backward draws the
+ * mask again from x, which needs K a multiple of 128; fp16 and fp32 need h).
  * Dropout keeps element i of the flattened [S, K] input by a hash of
  * (seed, i) with probability 1 - round(65536 p) / 65536 and scales kept
- * elements by 1 / (1 - p). K must be a multiple of 16; x, lora_A and h are read
- * or written with 16-byte vectors (aligned rows, strides multiples of 8).
- * workspace: mga_gated_lora_workspace_bytes(S, K, N, rank) bytes.
- * The plain GEMMs run in hipBLASLt on the same stream.
+ * elements by 1 / (1 - p). K must be a multiple of 16; with bf16, x, lora_A
+ * and h are read or written with 16-byte vectors (aligned rows, strides
+ * multiples of 8). workspace: mga_gated_lora_workspace_bytes(S, K, N, rank)
+ * bytes. bf16 runs the HIP down-projection kernel (dropout, scaling and gate
+ * fused); fp16 and fp32 run every product in hipBLASLt in the operand type
+ * (fp32 compute) with HIP kernels for the dropout and the row scaling. The
+ * plain GEMMs run in hipBLASLt on the same stream.
  */
 int64_t mga_gated_lora_workspace_bytes(int32_t S, int32_t K, int32_t N, int32_t rank);
 int mga_gated_lora_fwd(const void *x, int64_t x_rs, const void *weight, int64_t w_rs,
@@ -290,7 +295,7 @@ int mga_gated_lora_fwd(const void *x, int64_t x_rs, const void *weight, int64_t 
                        const float *gate, float scaling, double dropout_p, uint64_t seed,
                        int32_t S, int32_t K, int32_t N, int32_t rank,
                        void *y, int64_t y_rs, void *t, int64_t t_rs, void *h, int64_t h_rs,
-                       void *workspace, int64_t workspace_bytes, void *stream);
+                       void *workspace, int64_t workspace_bytes, int32_t dtype, void *stream);
 
 /*
  * Backward of mga_gated_lora_fwd (the autograd backward of the reference's
@@ -299,14 +304,14 @@ int mga_gated_lora_fwd(const void *x, int64_t x_rs, const void *weight, int64_t 
  *   grad_B = grad_y^T t,  d_a = T(T((grad_y B) * gate) * scaling),
  *   grad_x = T(grad_y W + T(mask * T(d_a A) / (1 - p))),  grad_A = d_a^T h.
  * grad_x, grad_a, grad_b may be NULL to skip them; h may be NULL when the
- * forward kept no dropout output (grad_A then recomputes it from x and the
- * seed; K a multiple of 128). With dropout on, grad_x is written with
- * vector accesses: its start must be 16-byte aligned and its row stride a
- * multiple of 4 (of 8 for the 16-byte path). grad_y B and grad_y^T t run as
- * one streaming pass over grad_y each (fp32 split sums added in a fixed
- * order) when rank <= 128, N is a multiple of 8 and grad_y, lora_B and t
- * have 16-byte aligned rows (strides multiples of 8); otherwise in
- * hipBLASLt, as grad_y W is.
+ * forward kept no dropout output (bf16: grad_A then recomputes it from x
+ * and the seed; K a multiple of 128). With bf16 and dropout on, grad_x is
+ * written with vector accesses: its start must be 16-byte aligned and its
+ * row stride a multiple of 4 (of 8 for the 16-byte path). With bf16, grad_y B
+ * and grad_y^T t run as one streaming pass over grad_y each (fp32 split sums
+ * added in a fixed order) when rank <= 128, N is a multiple of 8 and grad_y,
+ * lora_B and t have 16-byte aligned rows (strides multiples of 8); otherwise,
+ * and for fp16 and fp32, in hipBLASLt, as grad_y W is.
  */
 int mga_gated_lora_bwd(const void *grad_y, int64_t gy_rs, const void *x, int64_t x_rs,
                        const void *h, int64_t h_rs, const void *weight, int64_t w_rs,
@@ -315,7 +320,7 @@ int mga_gated_lora_bwd(const void *grad_y, int64_t gy_rs, const void *x, int64_t
                        double dropout_p, uint64_t seed, int32_t S, int32_t K, int32_t N, int32_t rank,
                        void *grad_x, int64_t gx_rs, void *grad_a, int64_t ga_rs,
                        void *grad_b, int64_t gb_rs, void *workspace, int64_t workspace_bytes,
-                       void *stream);
+                       int32_t dtype, void *stream);
 
 /*
  * Stable soft cross-entropy of the MTP sampler loss, row by row over n_rows

@@ -62,9 +62,9 @@ SIGNATURES = {
                              _P, _I64, _I64, _P, _I64, _I64, _P],
     "mga_gated_lora_workspace_bytes": [_I32, _I32, _I32, _I32],
     "mga_gated_lora_fwd": [_P, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _F32, _F64, _U64,
-                           _I32, _I32, _I32, _I32, _P, _I64, _P, _I64, _P, _I64, _P, _I64, _P],
+                           _I32, _I32, _I32, _I32, _P, _I64, _P, _I64, _P, _I64, _P, _I64, _I32, _P],
     "mga_gated_lora_bwd": [_P, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _F32,
-                           _F64, _U64, _I32, _I32, _I32, _I32, _P, _I64, _P, _I64, _P, _I64, _P, _I64, _P],
+                           _F64, _U64, _I32, _I32, _I32, _I32, _P, _I64, _P, _I64, _P, _I64, _P, _I64, _I32, _P],
     "mga_soft_ce_workspace_floats": [_I32, _I32],
     "mga_soft_ce_fwd": [_P, _I64, _P, _I64, _I32, _I32, _I32, _P, _P, _P, _P],
     "mga_soft_ce_bwd": [_P, _I64, _P, _I64, _I32, _I32, _I32, _P, _P, _P, _I64, _P],

@@ -1,4 +1,4 @@
-// Plain bf16 GEMMs through hipBLASLt, in row-major terms.
+// Plain GEMMs through hipBLASLt (bf16, fp16 or fp32 operands), in row-major terms.
 //
 //   D[M, N] = op(A)[M, K] * op(B)[K, N] (+ D when accumulate), fp32 compute,
 //   op(A) = A ([M, K], row stride lda) or A^T (A stored [K, M]),
@@ -22,12 +22,12 @@ namespace mga {
 namespace {
 
 struct AlgoKey {
-  int dev;
+  int dev, dtype;
   bool ta, tb, acc;
   int64_t m, n, k, lda, ldb, ldd;
   bool operator<(const AlgoKey &o) const {
-    return std::tie(dev, ta, tb, acc, m, n, k, lda, ldb, ldd) <
-           std::tie(o.dev, o.ta, o.tb, o.acc, o.m, o.n, o.k, o.lda, o.ldb, o.ldd);
+    return std::tie(dev, dtype, ta, tb, acc, m, n, k, lda, ldb, ldd) <
+           std::tie(o.dev, o.dtype, o.ta, o.tb, o.acc, o.m, o.n, o.k, o.lda, o.ldb, o.ldd);
   }
 };
 
@@ -56,10 +56,11 @@ const char *status_name(hipblasStatus_t s) {
 
 }  // namespace
 
-int gemm_bf16(bool ta, bool tb, int64_t M, int64_t N, int64_t K, const void *A, int64_t lda, const void *B,
-              int64_t ldb, bool accumulate, void *D, int64_t ldd, void *workspace, size_t ws_bytes,
-              hipStream_t stream, const char **err) {
+int gemm(int dtype, bool ta, bool tb, int64_t M, int64_t N, int64_t K, const void *A, int64_t lda, const void *B,
+         int64_t ldb, bool accumulate, void *D, int64_t ldd, void *workspace, size_t ws_bytes, hipStream_t stream,
+         const char **err) {
   *err = nullptr;
+  const hipDataType dt = dtype == kDtF16 ? HIP_R_16F : (dtype == kDtF32 ? HIP_R_32F : HIP_R_16BF);
   if (M == 0 || N == 0) return 0;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) {
@@ -77,7 +78,7 @@ int gemm_bf16(bool ta, bool tb, int64_t M, int64_t N, int64_t K, const void *A, 
     }
     h = g_handles.emplace(dev, hd).first;
   }
-  const AlgoKey key{dev, ta, tb, accumulate, M, N, K, lda, ldb, ldd};
+  const AlgoKey key{dev, dtype, ta, tb, accumulate, M, N, K, lda, ldb, ldd};
   auto it = g_plans.find(key);
   if (it == g_plans.end()) {
     Plan p;
@@ -95,9 +96,9 @@ int gemm_bf16(bool ta, bool tb, int64_t M, int64_t N, int64_t K, const void *A, 
     // stored (column-major) shapes of the swapped operands
     const uint64_t a_rows = tb ? K : N, a_cols = tb ? N : K;   // B buffer
     const uint64_t b_rows = ta ? M : K, b_cols = ta ? K : M;   // A buffer
-    if ((st = hipblasLtMatrixLayoutCreate(&p.la, HIP_R_16BF, a_rows, a_cols, ldb)) != HIPBLAS_STATUS_SUCCESS ||
-        (st = hipblasLtMatrixLayoutCreate(&p.lb, HIP_R_16BF, b_rows, b_cols, lda)) != HIPBLAS_STATUS_SUCCESS ||
-        (st = hipblasLtMatrixLayoutCreate(&p.ld, HIP_R_16BF, N, M, ldd)) != HIPBLAS_STATUS_SUCCESS) {
+    if ((st = hipblasLtMatrixLayoutCreate(&p.la, dt, a_rows, a_cols, ldb)) != HIPBLAS_STATUS_SUCCESS ||
+        (st = hipblasLtMatrixLayoutCreate(&p.lb, dt, b_rows, b_cols, lda)) != HIPBLAS_STATUS_SUCCESS ||
+        (st = hipblasLtMatrixLayoutCreate(&p.ld, dt, N, M, ldd)) != HIPBLAS_STATUS_SUCCESS) {
       *err = status_name(st);
       return -1;
     }
@@ -130,6 +131,12 @@ int gemm_bf16(bool ta, bool tb, int64_t M, int64_t N, int64_t K, const void *A, 
     return -1;
   }
   return 0;
+}
+
+int gemm_bf16(bool ta, bool tb, int64_t M, int64_t N, int64_t K, const void *A, int64_t lda, const void *B,
+              int64_t ldb, bool accumulate, void *D, int64_t ldd, void *workspace, size_t ws_bytes,
+              hipStream_t stream, const char **err) {
+  return gemm(kDtBf16, ta, tb, M, N, K, A, lda, B, ldb, accumulate, D, ldd, workspace, ws_bytes, stream, err);
 }
 
 }  // namespace mga

@@ -408,7 +408,7 @@ struct LoraWs {
 //  lora_B's backward products: 8 x max(S, N) x rpad fp32]
 int64_t lora_ws_bytes(int32_t S, int32_t K, int32_t N, int32_t rank) {
   const int64_t rp = lora_rpad(rank);
-  return kBlasWorkspace + 2 * align256((int64_t)S * rp * 2) + align256((int64_t)K * rp * 2) +
+  return kBlasWorkspace + 2 * align256((int64_t)S * rp * 4) + align256((int64_t)K * rp * 2) +
          align256((int64_t)8 * S * 96 * 4) + align256((int64_t)K / 16 * 3 * 1024) +
          align256((int64_t)mga::kDaMaxSplit * rp * K * 4) +
          align256((int64_t)mga::kSkinnyMaxSplit * std::max(S, N) * rp * 4);
@@ -420,8 +420,8 @@ LoraWs lora_ws(void *ws, int32_t S, int32_t K, int32_t rank) {
   LoraWs w;
   w.blas = p;
   w.u = p + kBlasWorkspace;
-  w.da = static_cast<char *>(w.u) + align256((int64_t)S * rp * 2);
-  w.at = static_cast<char *>(w.da) + align256((int64_t)S * rp * 2);
+  w.da = static_cast<char *>(w.u) + align256((int64_t)S * rp * 4);
+  w.at = static_cast<char *>(w.da) + align256((int64_t)S * rp * 4);
   w.part = reinterpret_cast<float *>(static_cast<char *>(w.at) + align256((int64_t)K * rp * 2));
   w.packed = reinterpret_cast<char *>(w.part) + align256((int64_t)8 * S * 96 * 4);
   w.dapart = reinterpret_cast<float *>(static_cast<char *>(w.packed) + align256((int64_t)K / 16 * 3 * 1024));
@@ -458,11 +458,76 @@ uint32_t drop_threshold(double p) { return (uint32_t)llround(p * 65536.0); }
 float keep_scale(double p) { return (float)(1.0 / (1.0 - p)); }
 
 int blas(const char *fn, bool ta, bool tb, int64_t M, int64_t N, int64_t K, const void *A, int64_t lda, const void *B,
-         int64_t ldb, bool acc, void *D, int64_t ldd, const LoraWs &w, hipStream_t st) {
+         int64_t ldb, bool acc, void *D, int64_t ldd, const LoraWs &w, hipStream_t st, int dtype = MGA_DTYPE_BF16) {
   const char *err = nullptr;
-  if (mga::gemm_bf16(ta, tb, M, N, K, A, lda, B, ldb, acc, D, ldd, w.blas, (size_t)kBlasWorkspace, st, &err))
+  if (mga::gemm(dtype, ta, tb, M, N, K, A, lda, B, ldb, acc, D, ldd, w.blas, (size_t)kBlasWorkspace, st, &err))
     return fail(MGA_ERR_HIP, "%s: hipBLASLt GEMM (%lld x %lld x %lld): %s", fn, (long long)M, (long long)N,
                 (long long)K, err ? err : "error");
+  return MGA_OK;
+}
+
+// fp16 / fp32 operands: hipBLASLt GEMMs in the operand type and the
+// elementwise kernels of the general path; the dropout output h is always
+// written (the backward's grad_A reads it).
+int gated_lora_fwd_general(const char *fn, int dtype, const void *x, int64_t x_rs, const void *weight, int64_t w_rs,
+                           const void *lora_a, int64_t a_rs, const void *lora_b, int64_t b_rs, const float *gate,
+                           float scaling, double dropout_p, uint64_t seed, int32_t S, int32_t K, int32_t N,
+                           int32_t rank, void *y, int64_t y_rs, void *t, int64_t t_rs, void *h, int64_t h_rs,
+                           const LoraWs &w, hipStream_t st) {
+  int rc;
+  const uint32_t thr = drop_threshold(dropout_p);
+  if (thr && (rc = check_rows_ld(fn, "dropout output h", h, h_rs, K))) return rc;
+  const void *src = x;
+  int64_t src_rs = x_rs;
+  if (thr) {   // h = dropout(x)
+    mga::launch_lora_gen_dropout(dtype, x, x_rs, S, K, thr, keep_scale(dropout_p), seed, h, h_rs, st);
+    if ((rc = check_launch(fn)) != MGA_OK) return rc;
+    src = h;
+    src_rs = h_rs;
+  }
+  // t = T(T(s T(h A^T)) gate)
+  if ((rc = blas(fn, false, true, S, rank, K, src, src_rs, lora_a, a_rs, false, t, t_rs, w, st, dtype))) return rc;
+  mga::launch_lora_gen_scale_rows(dtype, t, t_rs, gate, scaling, false, S, rank, (int32_t)lora_rpad(rank), t, t_rs,
+                                  st);
+  if ((rc = check_launch(fn)) != MGA_OK) return rc;
+  // y = T(x W^T + T(t B^T))
+  if ((rc = blas(fn, false, true, S, N, rank, t, t_rs, lora_b, b_rs, false, y, y_rs, w, st, dtype))) return rc;
+  return blas(fn, false, true, S, N, K, x, x_rs, weight, w_rs, true, y, y_rs, w, st, dtype);
+}
+
+int gated_lora_bwd_general(const char *fn, int dtype, const void *grad_y, int64_t gy_rs, const void *x, int64_t x_rs,
+                           const void *h, int64_t h_rs, const void *weight, int64_t w_rs, const void *lora_a,
+                           int64_t a_rs, const void *lora_b, int64_t b_rs, const void *t, int64_t t_rs,
+                           const float *gate, float scaling, double dropout_p, uint64_t seed, int32_t S, int32_t K,
+                           int32_t N, int32_t rank, void *grad_x, int64_t gx_rs, void *grad_a, int64_t ga_rs,
+                           void *grad_b, int64_t gb_rs, const LoraWs &w, hipStream_t st) {
+  int rc;
+  const uint32_t thr = drop_threshold(dropout_p);
+  const int64_t rp = lora_rpad(rank);
+  if (grad_a && thr && !h)
+    return fail(MGA_ERR_INVALID, "%s: the dropout output h of the forward is needed for grad_A with fp16 / fp32", fn);
+  // d_a = T(T(T(dY B) gate) s)
+  if ((rc = blas(fn, false, false, S, rank, N, grad_y, gy_rs, lora_b, b_rs, false, w.u, rp, w, st, dtype))) return rc;
+  mga::launch_lora_gen_scale_rows(dtype, w.u, rp, gate, scaling, true, S, rank, (int32_t)rp, w.da, rp, st);
+  if ((rc = check_launch(fn)) != MGA_OK) return rc;
+  // dB = dY^T t
+  if (grad_b && (rc = blas(fn, true, false, N, rank, S, grad_y, gy_rs, t, t_rs, false, grad_b, gb_rs, w, st, dtype)))
+    return rc;
+  if (grad_x) {
+    // dX = T(dY W + T(mask T(d_a A) / (1 - p)))
+    if ((rc = blas(fn, false, false, S, K, rank, w.da, rp, lora_a, a_rs, false, grad_x, gx_rs, w, st, dtype)))
+      return rc;
+    if (thr) {
+      mga::launch_lora_gen_dx_mask(dtype, grad_x, gx_rs, S, K, thr, keep_scale(dropout_p), seed, st);
+      if ((rc = check_launch(fn)) != MGA_OK) return rc;
+    }
+    if ((rc = blas(fn, false, false, S, K, N, grad_y, gy_rs, weight, w_rs, true, grad_x, gx_rs, w, st, dtype)))
+      return rc;
+  }
+  // dA = d_a^T dropout(x)
+  if (grad_a && (rc = blas(fn, true, false, rank, K, S, w.da, rp, thr ? h : x, thr ? h_rs : x_rs, false, grad_a,
+                           ga_rs, w, st, dtype)))
+    return rc;
   return MGA_OK;
 }
 
@@ -478,10 +543,23 @@ int mga_gated_lora_fwd(const void *x, int64_t x_rs, const void *weight, int64_t 
                        int64_t a_rs, const void *lora_b, int64_t b_rs, const float *gate, float scaling,
                        double dropout_p, uint64_t seed, int32_t S, int32_t K, int32_t N, int32_t rank, void *y,
                        int64_t y_rs, void *t, int64_t t_rs, void *h, int64_t h_rs, void *workspace,
-                       int64_t workspace_bytes, void *stream) {
+                       int64_t workspace_bytes, int32_t dtype, void *stream) {
   const char *fn = "mga_gated_lora_fwd";
   int rc;
   if ((rc = check_lora_sizes(fn, S, K, N, rank, dropout_p)) != MGA_OK) return rc;
+  if (!elem_bytes(dtype)) return fail(MGA_ERR_INVALID, "%s: unknown dtype code %d", fn, dtype);
+  if (dtype != MGA_DTYPE_BF16) {
+    const int64_t rp = lora_rpad(rank);
+    if ((rc = check_rows_ld(fn, "x", x, x_rs, K)) || (rc = check_rows_ld(fn, "weight", weight, w_rs, K)) ||
+        (rc = check_rows_ld(fn, "lora_A", lora_a, a_rs, K)) || (rc = check_rows_ld(fn, "lora_B", lora_b, b_rs, rank)) ||
+        (rc = check_rows_ld(fn, "output", y, y_rs, N)) || (rc = check_rows_ld(fn, "t", t, t_rs, rp)))
+      return rc;
+    if (!workspace || workspace_bytes < lora_ws_bytes(S, K, N, rank))
+      return fail(MGA_ERR_INVALID, "%s: workspace of %lld bytes needed", fn, (long long)lora_ws_bytes(S, K, N, rank));
+    return gated_lora_fwd_general(fn, dtype, x, x_rs, weight, w_rs, lora_a, a_rs, lora_b, b_rs, gate, scaling,
+                                  dropout_p, seed, S, K, N, rank, y, y_rs, t, t_rs, h, h_rs,
+                                  lora_ws(workspace, S, K, rank), (hipStream_t)stream);
+  }
   const uint32_t thr = drop_threshold(dropout_p);
   const int64_t rp = lora_rpad(rank);
   if ((rc = check_vec_rows(fn, "x", x, x_rs, K)) != MGA_OK || (rc = check_rows_ld(fn, "weight", weight, w_rs, K)) ||
@@ -512,10 +590,31 @@ int mga_gated_lora_bwd(const void *grad_y, int64_t gy_rs, const void *x, int64_t
                        int64_t b_rs, const void *t, int64_t t_rs, const float *gate, float scaling, double dropout_p,
                        uint64_t seed, int32_t S, int32_t K, int32_t N, int32_t rank, void *grad_x, int64_t gx_rs,
                        void *grad_a, int64_t ga_rs, void *grad_b, int64_t gb_rs, void *workspace,
-                       int64_t workspace_bytes, void *stream) {
+                       int64_t workspace_bytes, int32_t dtype, void *stream) {
   const char *fn = "mga_gated_lora_bwd";
   int rc;
   if ((rc = check_lora_sizes(fn, S, K, N, rank, dropout_p)) != MGA_OK) return rc;
+  if (!elem_bytes(dtype)) return fail(MGA_ERR_INVALID, "%s: unknown dtype code %d", fn, dtype);
+  if (dtype != MGA_DTYPE_BF16) {
+    const int64_t rp = lora_rpad(rank);
+    const bool thr = drop_threshold(dropout_p) != 0;
+    if ((rc = check_rows_ld(fn, "grad_output", grad_y, gy_rs, N)) ||
+        (rc = check_rows_ld(fn, "lora_B", lora_b, b_rs, rank)) || (rc = check_rows_ld(fn, "t", t, t_rs, rp)))
+      return rc;
+    if (grad_x && ((rc = check_rows_ld(fn, "weight", weight, w_rs, K)) ||
+                   (rc = check_rows_ld(fn, "lora_A", lora_a, a_rs, K)) ||
+                   (rc = check_rows_ld(fn, "grad_x", grad_x, gx_rs, K))))
+      return rc;
+    if (grad_a && ((rc = check_rows_ld(fn, "grad_A", grad_a, ga_rs, K)) ||
+                   (!thr && (rc = check_rows_ld(fn, "x", x, x_rs, K)))))
+      return rc;
+    if (grad_b && (rc = check_rows_ld(fn, "grad_B", grad_b, gb_rs, rank))) return rc;
+    if (!workspace || workspace_bytes < lora_ws_bytes(S, K, N, rank))
+      return fail(MGA_ERR_INVALID, "%s: workspace of %lld bytes needed", fn, (long long)lora_ws_bytes(S, K, N, rank));
+    return gated_lora_bwd_general(fn, dtype, grad_y, gy_rs, x, x_rs, h, h_rs, weight, w_rs, lora_a, a_rs, lora_b, b_rs,
+                                  t, t_rs, gate, scaling, dropout_p, seed, S, K, N, rank, grad_x, gx_rs, grad_a,
+                                  ga_rs, grad_b, gb_rs, lora_ws(workspace, S, K, rank), (hipStream_t)stream);
+  }
   const uint32_t thr = drop_threshold(dropout_p);
   const int64_t rp = lora_rpad(rank);
   if ((rc = check_rows_ld(fn, "grad_output", grad_y, gy_rs, N)) ||

@@ -77,9 +77,13 @@ struct QkRopeArgs {
 };
 void launch_qk_norm_rope(const QkRopeArgs &a, int dtype, bool backward, hipStream_t stream);
 
-// Plain bf16 GEMM through hipBLASLt, row-major (mga_blas.hip):
+// Plain GEMM through hipBLASLt, row-major (mga_blas.hip), operands and
+// output of one element type (kDt*), fp32 compute:
 // D[M, N] = op(A)[M, K] op(B)[K, N] (+ D), op(A) = A^T when ta (A stored
 // [K, M]), op(B) = B^T when tb (B stored [N, K]). Returns 0, or -1 with *err set.
+int gemm(int dtype, bool ta, bool tb, int64_t M, int64_t N, int64_t K, const void *A, int64_t lda, const void *B,
+         int64_t ldb, bool accumulate, void *D, int64_t ldd, void *workspace, size_t ws_bytes, hipStream_t stream,
+         const char **err);
 int gemm_bf16(bool ta, bool tb, int64_t M, int64_t N, int64_t K, const void *A, int64_t lda, const void *B,
               int64_t ldb, bool accumulate, void *D, int64_t ldd, void *workspace, size_t ws_bytes,
               hipStream_t stream, const char **err);
@@ -138,6 +142,19 @@ void launch_lora_scale_rows(const void *u, int64_t u_rs, const float *gate, floa
                             int32_t rank, int32_t rpad, void *da, int64_t da_rs, hipStream_t stream);
 void launch_lora_transpose(const void *A, int64_t a_rs, int32_t rank, int32_t K, int32_t rpad, void *At,
                            int64_t at_rs, hipStream_t stream);
+// The general path (fp16 and fp32 operands, dtype kDtF16 / kDtF32): the
+// elementwise steps around its hipBLASLt GEMMs, with the bf16 path's dropout
+// bits (element pair j of the flattened [S, K] input, same hash and seed).
+// h = T(x / (1 - p)) where kept, else 0.
+void launch_lora_gen_dropout(int dtype, const void *x, int64_t x_rs, int32_t S, int32_t K, uint32_t thr,
+                             float keep_scale, uint64_t seed, void *h, int64_t h_rs, hipStream_t stream);
+// out = T(T(u * gate) * scaling) (gate_first) or T(T(u * scaling) * gate), rows
+// of rank entries then zeros up to rpad (may be in place).
+void launch_lora_gen_scale_rows(int dtype, const void *u, int64_t u_rs, const float *gate, float scaling, bool gate_first,
+                                int32_t S, int32_t rank, int32_t rpad, void *out, int64_t out_rs, hipStream_t stream);
+// dx = T(dx / (1 - p)) where kept, else 0 (in place).
+void launch_lora_gen_dx_mask(int dtype, void *dx, int64_t dx_rs, int32_t S, int32_t K, uint32_t thr, float keep_scale,
+                             uint64_t seed, hipStream_t stream);
 
 // Stable soft cross-entropy (mga_soft_ce.hip). Rows of V columns; row strides
 // in elements; vec: 16-byte vector loads (every row start 16-byte aligned).

@@ -1060,6 +1060,86 @@ void launch_lora_transpose(const void *A, int64_t a_rs, int32_t rank, int32_t K,
                      reinterpret_cast<const bf16_t *>(A), a_rs, rank, K, rpad, reinterpret_cast<bf16_t *>(At), at_rs);
 }
 
+// ---- the general path (fp16 / fp32 operands) ------------------------------
+// HBM-bound elementwise kernels: one thread per element pair (dropout) or
+// element (scale rows); the products run in hipBLASLt.
+
+namespace {
+
+template <typename T> __device__ __forceinline__ float to_f(T v) { return (float)v; }
+template <typename T> __device__ __forceinline__ T from_f(float v) { return (T)v; }
+
+template <typename T>
+__global__ __launch_bounds__(256) void lora_gen_dropout_kernel(const T *x, int64_t x_rs, int32_t S, int32_t K,
+                                                               uint32_t thr, float ks, uint64_t seed, T *h,
+                                                               int64_t h_rs, int32_t in_place) {
+  const int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;   // element pair of the flattened [S, K]
+  if (j >= (int64_t)S * K / 2) return;
+  const int64_t e = 2 * j;
+  const int s = (int)(e / K), k = (int)(e - (int64_t)s * K);   // K is even: the pair stays in the row
+  const uint32_t bits = pair_bits(seed, (uint64_t)j);
+  const T *xr = in_place ? h + (int64_t)s * h_rs : x + (int64_t)s * x_rs;
+  T *hr = h + (int64_t)s * h_rs;
+  const float v0 = to_f(xr[k]), v1 = to_f(xr[k + 1]);
+  hr[k] = (bits & 0xffffu) >= thr ? from_f<T>(v0 * ks) : from_f<T>(0.f);
+  hr[k + 1] = (bits >> 16) >= thr ? from_f<T>(v1 * ks) : from_f<T>(0.f);
+}
+
+// rows of rank entries, then zeros up to rpad (the padded columns the bf16
+// kernels write as zeros too)
+template <typename T>
+__global__ __launch_bounds__(256) void lora_gen_scale_rows_kernel(const T *u, int64_t u_rs, const float *gate,
+                                                                  float scaling, int32_t gate_first, int32_t S,
+                                                                  int32_t rank, int32_t rpad, T *out, int64_t out_rs) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)S * rpad) return;
+  const int s = (int)(i / rpad), r = (int)(i - (int64_t)s * rpad);
+  float w = 0.f;
+  if (r < rank) {
+    const float g = gate ? gate[s] : 1.f;
+    const float v = to_f(u[(int64_t)s * u_rs + r]);
+    w = gate_first ? to_f(from_f<T>(to_f(from_f<T>(v * g)) * scaling))
+                   : to_f(from_f<T>(to_f(from_f<T>(v * scaling)) * g));
+  }
+  out[(int64_t)s * out_rs + r] = from_f<T>(w);
+}
+
+template <typename T>
+void gen_launch(int64_t n, void (*k)(const T *, int64_t, int32_t, int32_t, uint32_t, float, uint64_t, T *, int64_t, int32_t),
+                const void *x, int64_t x_rs, int32_t S, int32_t K, uint32_t thr, float ks, uint64_t seed, void *h,
+                int64_t h_rs, int32_t in_place, hipStream_t st) {
+  hipLaunchKernelGGL(k, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, reinterpret_cast<const T *>(x), x_rs, S,
+                     K, thr, ks, seed, reinterpret_cast<T *>(h), h_rs, in_place);
+}
+
+}  // namespace
+
+void launch_lora_gen_dropout(int dtype, const void *x, int64_t x_rs, int32_t S, int32_t K, uint32_t thr,
+                             float keep_scale, uint64_t seed, void *h, int64_t h_rs, hipStream_t st) {
+  const int64_t n = (int64_t)S * K / 2;
+  if (dtype == kDtF32) gen_launch<float>(n, lora_gen_dropout_kernel<float>, x, x_rs, S, K, thr, keep_scale, seed, h, h_rs, 0, st);
+  else gen_launch<f16_t>(n, lora_gen_dropout_kernel<f16_t>, x, x_rs, S, K, thr, keep_scale, seed, h, h_rs, 0, st);
+}
+
+void launch_lora_gen_dx_mask(int dtype, void *dx, int64_t dx_rs, int32_t S, int32_t K, uint32_t thr, float keep_scale,
+                             uint64_t seed, hipStream_t st) {
+  const int64_t n = (int64_t)S * K / 2;
+  if (dtype == kDtF32) gen_launch<float>(n, lora_gen_dropout_kernel<float>, dx, dx_rs, S, K, thr, keep_scale, seed, dx, dx_rs, 1, st);
+  else gen_launch<f16_t>(n, lora_gen_dropout_kernel<f16_t>, dx, dx_rs, S, K, thr, keep_scale, seed, dx, dx_rs, 1, st);
+}
+
+void launch_lora_gen_scale_rows(int dtype, const void *u, int64_t u_rs, const float *gate, float scaling, bool gate_first,
+                                int32_t S, int32_t rank, int32_t rpad, void *out, int64_t out_rs, hipStream_t st) {
+  const int64_t n = (int64_t)S * rpad;
+  const dim3 grid((unsigned)((n + 255) / 256));
+  if (dtype == kDtF32)
+    hipLaunchKernelGGL(lora_gen_scale_rows_kernel<float>, grid, dim3(256), 0, st, reinterpret_cast<const float *>(u),
+                       u_rs, gate, scaling, (int32_t)gate_first, S, rank, rpad, reinterpret_cast<float *>(out), out_rs);
+  else
+    hipLaunchKernelGGL(lora_gen_scale_rows_kernel<f16_t>, grid, dim3(256), 0, st, reinterpret_cast<const f16_t *>(u),
+                       u_rs, gate, scaling, (int32_t)gate_first, S, rank, rpad, reinterpret_cast<f16_t *>(out), out_rs);
+}
+
 namespace {
 
 // splits of the reduced dimension: about two workgroups per CU, at most

@@ -22,10 +22,13 @@ and gate are applied to the rank-r activations before lora_B rather than to
 lora_B's output (the same value when the scaling is a power of two and the
 gate is 0 / 1, as in the reference's configurations), and the base product
 is accumulated in fp32 onto the rounded LoRA term before one final rounding
-(in the backward likewise for dX). bf16 only: GatedLoRALinear and
-apply_lora_to_model raise TypeError for a base layer of another dtype (before
-apply_lora_to_model changes anything); no biases (Qwen3 and Llama
-projections have none), base weights frozen.
+(in the backward likewise for dX). bf16, fp16 and fp32 layers (the
+reference's model dtypes, args.py:15): bf16 runs the HIP down-projection and
+streaming backward kernels; fp16 and fp32 run every product in hipBLASLt in
+the layer's dtype with HIP kernels for the dropout (the same mask) and the
+row scaling, and keep the dropout output for grad_A. Other dtypes raise
+TypeError (before apply_lora_to_model changes anything); no biases (Qwen3
+and Llama projections have none), base weights frozen.
 """
 from __future__ import annotations
 
@@ -44,11 +47,14 @@ def _rpad(rank: int) -> int:
     return (rank + 31) // 32 * 32
 
 
-def _rows(name: str, t: torch.Tensor, cols: int) -> torch.Tensor:
-    """A [rows, cols] bf16 view whose rows suit 16-byte vector access."""
+DTYPES = {torch.bfloat16: _lib.DTYPE_BF16, torch.float16: _lib.DTYPE_F16, torch.float32: _lib.DTYPE_F32}
+
+
+def _rows(name: str, t: torch.Tensor, cols: int, dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    """A [rows, cols] view of ``dtype`` whose rows suit 16-byte vector access."""
     _dev(name, t)
-    if t.dtype != torch.bfloat16:
-        raise TypeError(f"{name}: bfloat16 required (got {t.dtype})")
+    if t.dtype != dtype:
+        raise TypeError(f"{name}: {dtype} required (got {t.dtype})")
     if t.shape[-1] != cols:
         raise ValueError(f"{name}: last dimension {t.shape[-1]} != {cols}")
     v = t.reshape(-1, cols)
@@ -78,17 +84,18 @@ def gated_lora_forward(x2, weight, lora_a, lora_b, gate, scaling: float, p: floa
     multiple of 128 (the backward otherwise draws the mask again from x2)."""
     S, K = x2.shape
     N, rank = weight.shape[0], lora_a.shape[0]
-    dev = x2.device
-    y = torch.empty(S, N, device=dev, dtype=torch.bfloat16)
-    t = torch.empty(S, _rpad(rank), device=dev, dtype=torch.bfloat16)
-    h = torch.empty(S, K, device=dev, dtype=torch.bfloat16) if p > 0 and (keep_h or K % 128) else None
+    dev, dt = x2.device, x2.dtype
+    y = torch.empty(S, N, device=dev, dtype=dt)
+    t = torch.empty(S, _rpad(rank), device=dev, dtype=dt)
+    # the general path (fp16 / fp32) always keeps h: its grad_A reads it
+    h = torch.empty(S, K, device=dev, dtype=dt) if p > 0 and (keep_h or K % 128 or dt != torch.bfloat16) else None
     ws = _workspace(S, K, N, rank, dev)
     _lib.call("mga_gated_lora_fwd", x2.data_ptr(), x2.stride(0), weight.data_ptr(), weight.stride(0),
               lora_a.data_ptr(), lora_a.stride(0), lora_b.data_ptr(), lora_b.stride(0),
               gate.data_ptr() if gate is not None else None, float(scaling), float(p), seed,
               S, K, N, rank, y.data_ptr(), y.stride(0), t.data_ptr(), t.stride(0),
               h.data_ptr() if h is not None else None, h.stride(0) if h is not None else 0,
-              ws.data_ptr(), ws.numel(), _stream(x2))
+              ws.data_ptr(), ws.numel(), DTYPES[dt], _stream(x2))
     return y, t, h
 
 
@@ -96,10 +103,10 @@ def gated_lora_backward(gy2, x2, h, t, weight, lora_a, lora_b, gate, scaling: fl
                         need_x: bool, need_a: bool, need_b: bool):
     S, K = x2.shape
     N, rank = weight.shape[0], lora_a.shape[0]
-    dev = x2.device
-    gx = torch.empty(S, K, device=dev, dtype=torch.bfloat16) if need_x else None
-    ga = torch.empty(rank, K, device=dev, dtype=torch.bfloat16) if need_a else None
-    gb = torch.empty(N, rank, device=dev, dtype=torch.bfloat16) if need_b else None
+    dev, dt = x2.device, x2.dtype
+    gx = torch.empty(S, K, device=dev, dtype=dt) if need_x else None
+    ga = torch.empty(rank, K, device=dev, dtype=dt) if need_a else None
+    gb = torch.empty(N, rank, device=dev, dtype=dt) if need_b else None
     ws = _workspace(S, K, N, rank, dev)
     ptr = lambda v: v.data_ptr() if v is not None else None   # noqa: E731
     rs = lambda v: v.stride(0) if v is not None else 0         # noqa: E731
@@ -107,7 +114,7 @@ def gated_lora_backward(gy2, x2, h, t, weight, lora_a, lora_b, gate, scaling: fl
               weight.data_ptr(), weight.stride(0), lora_a.data_ptr(), lora_a.stride(0), lora_b.data_ptr(),
               lora_b.stride(0), t.data_ptr(), t.stride(0), ptr(gate), float(scaling), float(p), seed,
               S, K, N, rank, ptr(gx), rs(gx), ptr(ga), rs(ga), ptr(gb), rs(gb),
-              ws.data_ptr(), ws.numel(), _stream(x2))
+              ws.data_ptr(), ws.numel(), DTYPES[dt], _stream(x2))
     return gx, ga, gb
 
 
@@ -115,11 +122,14 @@ class _GatedLoRA(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, weight, lora_a, lora_b, gate_mask, scaling, p, seed):
         K = weight.shape[1]
-        x2 = _rows("x", x, K)
+        dt = weight.dtype
+        if dt not in DTYPES:
+            raise TypeError(f"weight: bfloat16, float16 or float32 required (got {dt})")
+        x2 = _rows("x", x, K, dt)
         for name, w in (("weight", weight), ("lora_A.weight", lora_a), ("lora_B.weight", lora_b)):
             _dev(name, w)
-            if w.dtype != torch.bfloat16:
-                raise TypeError(f"{name}: bfloat16 required (got {w.dtype})")
+            if w.dtype != dt:
+                raise TypeError(f"{name}: {dt} required (got {w.dtype})")
         weight, lora_a, lora_b = weight.contiguous(), lora_a.contiguous(), lora_b.contiguous()
         if lora_a.shape[1] != K or lora_b.shape != (weight.shape[0], lora_a.shape[0]):
             raise ValueError(f"shapes: weight {tuple(weight.shape)}, lora_A {tuple(lora_a.shape)}, "
@@ -134,7 +144,7 @@ class _GatedLoRA(torch.autograd.Function):
     def backward(ctx, gy):
         x2, h, t, weight, lora_a, lora_b, gate = ctx.saved_tensors
         scaling, p, seed, xshape = ctx.meta
-        gy2 = _rows("grad_output", gy, weight.shape[0])
+        gy2 = _rows("grad_output", gy.to(weight.dtype), weight.shape[0], weight.dtype)
         gx, ga, gb = gated_lora_backward(gy2, x2, h, t, weight, lora_a, lora_b, gate, scaling, p, seed,
                                          ctx.needs_input_grad[0], ctx.needs_input_grad[2],
                                          ctx.needs_input_grad[3])
@@ -180,9 +190,9 @@ class GatedLoRALinear(nn.Module):
 
 
 def _check_base_dtype(name: str, layer: nn.Linear) -> None:
-    if layer.weight.dtype != torch.bfloat16:
-        raise TypeError(f"{name}: the fused gated LoRA layer supports bfloat16 base layers only "
-                        f"(got {layer.weight.dtype}); convert the model with .to(torch.bfloat16) first")
+    if layer.weight.dtype not in DTYPES:
+        raise TypeError(f"{name}: the fused gated LoRA layer supports bfloat16, float16 and float32 base "
+                        f"layers (got {layer.weight.dtype})")
 
 
 def _freeze_base_and_enable_lora(model: nn.Module) -> None:

@@ -20,6 +20,12 @@ roundings of 2^-9):
   for bit.
 The full Qwen3-8B qkv shape (S = 5120) is compared with an fp32 torch
 reference on the GPU under the same bounds.
+
+fp16 and fp32 layers (the reference's other model dtypes, args.py:15) run the
+general path (hipBLASLt products in the layer's dtype, HIP dropout and row
+scaling): the same bounds with u = 2^-10 for fp16; for fp32, u = 2^-18 and
+the same u on the sums of absolute products, which covers fp32 accumulation
+over K = 4096 terms.
 """
 import importlib
 
@@ -31,18 +37,21 @@ from oracle import gated_lora as gl
 
 pytestmark = pytest.mark.gpu
 U = 2.0 ** -8
+# rounding unit per dtype; ACC: the bound's factor on sums of absolute
+# products (fp32 accumulation error), 0 where the roundings dominate
+UNIT = {torch.bfloat16: (2.0 ** -8, 0.0), torch.float16: (2.0 ** -10, 0.0), torch.float32: (2.0 ** -18, 2.0 ** -18)}
 
 
 def lora_mod():
     return importlib.import_module("mtp-glora_amd.lora")
 
 
-def make(S, K, N, r, dev, seed=0, gate="mixed"):
+def make(S, K, N, r, dev, seed=0, gate="mixed", dtype=torch.bfloat16):
     g = torch.Generator(device=dev).manual_seed(seed)
-    x = torch.randn(S, K, generator=g, device=dev).bfloat16()
-    W = (torch.randn(N, K, generator=g, device=dev) / K ** 0.5).bfloat16()
-    A = (torch.randn(r, K, generator=g, device=dev) / K ** 0.5).bfloat16()
-    B = (torch.randn(N, r, generator=g, device=dev) * (0.5 / r ** 0.5)).bfloat16()
+    x = torch.randn(S, K, generator=g, device=dev).to(dtype)
+    W = (torch.randn(N, K, generator=g, device=dev) / K ** 0.5).to(dtype)
+    A = (torch.randn(r, K, generator=g, device=dev) / K ** 0.5).to(dtype)
+    B = (torch.randn(N, r, generator=g, device=dev) * (0.5 / r ** 0.5)).to(dtype)
     gt = None if gate is None else (torch.rand(S, generator=g, device=dev) < 0.7).float()
     return x, W, A, B, gt
 
@@ -58,17 +67,19 @@ def check(name, got, ref, bound):
     assert worst <= 1.0, name
 
 
-def run_case(dev, S, K, N, r, p, gate="mixed", seed=0, scaling=2.0):
-    """The layer's own path (no dropout output kept when K is a multiple of
-    128: grad_A draws the mask again from x), checked against the oracle; with
-    dropout on, also the path that keeps h: h bit for bit, the same y, and a
-    grad_A from hipBLASLt over h that meets the same bound."""
+def run_case(dev, S, K, N, r, p, gate="mixed", seed=0, scaling=2.0, dtype=torch.bfloat16):
+    """The layer's own path (bf16: no dropout output kept when K is a multiple
+    of 128, grad_A draws the mask again from x), checked against the oracle;
+    with dropout on, also the path that keeps h: h bit for bit, the same y,
+    and a grad_A over h that meets the same bound."""
     lm = lora_mod()
-    x, W, A, B, gt = make(S, K, N, r, dev, seed, gate)
+    U, ACC = UNIT[dtype]
+    x, W, A, B, gt = make(S, K, N, r, dev, seed, gate, dtype)
     sd = 1234567 + seed
     y, t, h = lm.gated_lora_forward(x, W, A, B, gt, scaling, p, sd)
-    assert h is None or K % 128 or p == 0
-    dy = torch.randn(S, N, generator=torch.Generator(device=dev).manual_seed(seed + 7), device=dev).bfloat16()
+    assert h is None or K % 128 or p == 0 or dtype != torch.bfloat16
+    assert (h is not None) == (p > 0) or dtype == torch.bfloat16
+    dy = torch.randn(S, N, generator=torch.Generator(device=dev).manual_seed(seed + 7), device=dev).to(dtype)
     gx, ga, gb = lm.gated_lora_backward(dy, x, h, t, W, A, B, gt, scaling, p, sd, True, True, True)
     if p > 0:
         yk, tk, hk = lm.gated_lora_forward(x, W, A, B, gt, scaling, p, sd, keep_h=True)
@@ -77,7 +88,7 @@ def run_case(dev, S, K, N, r, p, gate="mixed", seed=0, scaling=2.0):
     X, Wn, An, Bn, G, DY = f64(x), f64(W), f64(A), f64(B), f64(gt), f64(dy)
     keep = gl.keep_mask(sd, S, K, p) if p > 0 else None
     if p > 0:   # the kernel's dropout output, bit for bit, and the same forward with or without it
-        want = (keep * f64(x.float().mul(1.0 / (1.0 - p)).bfloat16()))
+        want = (keep * f64(x.float().mul(1.0 / (1.0 - p)).to(dtype)))
         np.testing.assert_array_equal(f64(hk), want)
         assert torch.equal(yk, y) and torch.equal(tk, t)
     Gv = np.ones(S) if G is None else G
@@ -85,12 +96,16 @@ def run_case(dev, S, K, N, r, p, gate="mixed", seed=0, scaling=2.0):
     ks = 1.0 if p == 0 else 1.0 / (1 - p)
     y_ref = gl.forward(X, Wn, An, Bn, G, scaling, keep, p)
     lora_abs = scaling * Gv[:, None] * (np.abs(H @ An.T) @ np.abs(Bn).T)
-    h_round = 0.0 if p == 0 else (U / 2) * scaling * Gv[:, None] * ((np.abs(H) @ np.abs(An).T) @ np.abs(Bn).T)
+    lora_sum = scaling * Gv[:, None] * ((np.abs(H) @ np.abs(An).T) @ np.abs(Bn).T)
+    h_round = 0.0 if p == 0 else (U / 2) * lora_sum
+    acc_y = ACC * (np.abs(X) @ np.abs(Wn).T + lora_sum)
     check("y", f64(y), y_ref,
-          U * (np.abs(y_ref) + np.abs(X @ Wn.T) + lora_abs) + h_round + 1e-5 * np.abs(y_ref).max())
+          U * (np.abs(y_ref) + np.abs(X @ Wn.T) + lora_abs) + h_round + acc_y + 1e-5 * np.abs(y_ref).max())
     dx_ref, dA_ref, dB_ref = gl.backward(DY, X, Wn, An, Bn, G, scaling, keep, p)
     d_a = scaling * Gv[:, None] * (DY @ Bn)
-    bx = U * (np.abs(dx_ref) + np.abs(DY @ Wn) + 2 * ks * (np.abs(d_a) @ np.abs(An))) + 1e-5 * np.abs(dx_ref).max()
+    acc_x = ACC * (np.abs(DY) @ np.abs(Wn) + 2 * ks * ((Gv[:, None] * scaling * (np.abs(DY) @ np.abs(Bn))) @ np.abs(An)))
+    bx = U * (np.abs(dx_ref) + np.abs(DY @ Wn) + 2 * ks * (np.abs(d_a) @ np.abs(An))) + acc_x \
+        + 1e-5 * np.abs(dx_ref).max()
     check("dX", f64(gx), dx_ref, bx)
     check("dA", f64(ga), dA_ref, U * (np.abs(dA_ref) + np.abs(d_a).T @ np.abs(H)) + 1e-30)
     if p > 0:
@@ -104,6 +119,22 @@ def run_case(dev, S, K, N, r, p, gate="mixed", seed=0, scaling=2.0):
 def test_qwen3_qkv_shape(dev, p):
     """Qwen3-8B fused qkv_proj with the reference's training ranks (3 x 32)."""
     run_case(dev, S=512, K=4096, N=6144, r=96, p=p)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("S,K,N,r,p,gate", [
+    (512, 4096, 6144, 96, 0.05, "mixed"),   # Qwen3-8B qkv_proj, dropout on
+    (512, 4096, 6144, 96, 0.0, "mixed"),
+    (333, 4096, 4096, 32, 0.05, None),      # o_proj-like, ragged rows, no gate
+    (40, 1024, 200, 64, 0.5, "mixed"),      # heavy dropout, odd N
+    (31, 128, 64, 1, 0.0, "mixed"),         # rank 1
+    (50, 272, 100, 24, 0.05, "mixed"),      # in_features not a multiple of 128
+])
+def test_fp16_fp32_layers(dev, dtype, S, K, N, r, p, gate):
+    """fp16 and fp32 layers through the general path against the float64
+    oracle, the dropout mask identical to the bf16 path's."""
+    print(f"case {dtype} S={S} K={K} N={N} r={r} p={p}", flush=True)
+    run_case(dev, S, K, N, r, p, gate=gate, seed=S + 1, dtype=dtype)
 
 
 @pytest.mark.parametrize("S,K,N,r,p,gate", [
@@ -140,23 +171,24 @@ def test_full_qkv_forward_against_fp32(dev):
     assert abs(kept - (1 - gl.drop_threshold(p) / 65536)) < 1e-3
 
 
-def test_module_forward_backward(dev):
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_module_forward_backward(dev, dtype):
     """GatedLoRALinear (the mirror) in train mode through autograd: x, lora_A
     and lora_B get gradients, the base weight none, and the result equals the
     functional entry points with the same seed."""
     lm = lora_mod()
     torch.manual_seed(0)
-    base = torch.nn.Linear(256, 384, bias=False).to(dev, torch.bfloat16)
+    base = torch.nn.Linear(256, 384, bias=False).to(dev, dtype)
     layer = lm.GatedLoRALinear(base, rank=16, alpha=32, dropout=0.05, lora_bias=False, use_rslora=False)
     base.weight.requires_grad_(False)
     with torch.no_grad():
         layer.lora_B.weight.normal_(0, 0.05)
-    x = torch.randn(1, 100, 256, device=dev).bfloat16().requires_grad_()
+    x = torch.randn(1, 100, 256, device=dev).to(dtype).requires_grad_()
     gate = (torch.rand(1, 100, 1, device=dev) < 0.5).long()
     torch.manual_seed(5)
     y = layer(x, gate)
     y.float().square().sum().backward()
-    assert y.shape == (1, 100, 384) and y.dtype == torch.bfloat16
+    assert y.shape == (1, 100, 384) and y.dtype == dtype
     assert x.grad is not None and layer.lora_A.weight.grad is not None and layer.lora_B.weight.grad is not None
     assert base.weight.grad is None
     torch.manual_seed(5)
@@ -203,7 +235,8 @@ def test_dx_row_stride_multiple_of_4(dev):
     lib.call("mga_gated_lora_bwd", dy.data_ptr(), dy.stride(0), x.data_ptr(), x.stride(0), None,
              0, W.data_ptr(), W.stride(0), A.data_ptr(), A.stride(0), B.data_ptr(), B.stride(0),
              t.data_ptr(), t.stride(0), gt.data_ptr(), s, p, sd, S, K, N, r, gx.data_ptr(), gx.stride(0),
-             None, 0, None, 0, ws.data_ptr(), ws.numel(), torch.cuda.current_stream(dev).cuda_stream)
+             None, 0, None, 0, ws.data_ptr(), ws.numel(), lib.DTYPE_BF16,
+             torch.cuda.current_stream(dev).cuda_stream)
     torch.cuda.synchronize()
     assert torch.count_nonzero(buf[:, K:]).item() == 0   # the 4 pad columns are untouched
     X, Wn, An, Bn, G, DY = f64(x), f64(W), f64(A), f64(B), f64(gt), f64(dy)

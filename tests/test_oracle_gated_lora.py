@@ -165,16 +165,26 @@ def test_apply_lora_to_model_wraps_and_freezes():
     assert not net.attn.qkv_proj.base_layer.weight.requires_grad
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
-def test_apply_lora_to_model_refuses_other_dtypes_up_front(dtype):
-    """The fused layer is bf16 only: a model of another dtype gets a TypeError
-    naming the first target layer, before any layer is wrapped or frozen."""
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+def test_apply_lora_to_model_wraps_every_model_dtype(dtype):
+    """bf16, fp16 and fp32 models (the reference's dtypes, args.py:15) are all
+    wrapped, the LoRA weights in the base layer's dtype."""
     mod = importlib.import_module("mtp-glora_amd")
     net = _lora_net(dtype)
-    net.mlp.down_proj.to(torch.bfloat16)   # one matching layer of the right dtype changes nothing
-    with pytest.raises(TypeError, match="attn.qkv_proj.*bfloat16"):
+    mod.apply_lora_to_model(net, rank=4, alpha=8, dropout=0.0)
+    assert isinstance(net.attn.qkv_proj, mod.GatedLoRALinear)
+    assert net.attn.qkv_proj.lora_A.weight.dtype == dtype and net.mlp.down_proj.lora_B.weight.dtype == dtype
+
+
+def test_apply_lora_to_model_refuses_other_dtypes_up_front():
+    """A dtype the layer has no path for (float64) gets a TypeError naming the
+    first target layer, before any layer is wrapped or frozen."""
+    mod = importlib.import_module("mtp-glora_amd")
+    net = _lora_net(torch.float64)
+    net.mlp.down_proj.to(torch.bfloat16)   # one matching layer of a supported dtype changes nothing
+    with pytest.raises(TypeError, match="attn.qkv_proj.*float64"):
         mod.apply_lora_to_model(net, rank=4, alpha=8, dropout=0.0)
     assert not any(isinstance(m, mod.GatedLoRALinear) for m in net.modules())
     assert all(p.requires_grad for p in net.parameters())
-    with pytest.raises(TypeError, match="bfloat16"):
-        mod.GatedLoRALinear(torch.nn.Linear(8, 8, bias=False, dtype=dtype), 4, 8, 0.0, False, False)
+    with pytest.raises(TypeError, match="float64"):
+        mod.GatedLoRALinear(torch.nn.Linear(8, 8, bias=False, dtype=torch.float64), 4, 8, 0.0, False, False)
