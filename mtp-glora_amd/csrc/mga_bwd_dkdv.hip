@@ -421,6 +421,9 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_kernel(AttnArgs a, 
             dsw[u][t] = (int)cvt2<E>(pv[r / 4][r % 4] * dprev[r], pv[(r + 1) / 4][(r + 1) % 4] * dprev[r + 1]);
           }
         const bf16_t *tQprev = qslot((J + 3) % 4);
+        // the dK and dP products at raised issue priority: the SIMD's A wave
+        // is then in its exponentials or its dV product (about 1 % on the pass)
+        __builtin_amdgcn_s_setprio(1);
         constexpr int NT = 2 * DB, AH = 3;
         bf16x8 ow[AH];
 #pragma unroll
@@ -446,6 +449,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_kernel(AttnArgs a, 
           if (ks + 1 < KS) op = nx;
         }
       }
+      __builtin_amdgcn_s_setprio(0);
       // this wave's loads of step j + 1 landed: all but Q(j + 2) just issued
       asm volatile("s_waitcnt vmcnt(%0)" : : "n"(kInst) : "memory");
       lds_barrier();

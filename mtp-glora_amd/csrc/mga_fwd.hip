@@ -354,7 +354,10 @@ __global__ __launch_bounds__(256 * NG, 2) void attn_fwd_kernel(AttnArgs a, int k
       }
       l_run += ps;
       // O^T += V^T P^T; operand t = (16-key slice t / DB, output block t % DB),
-      // read one ahead
+      // read one ahead. The wave issues at raised priority meanwhile, so the
+      // SIMD's other wave, usually in its softmax, yields it the issue slots
+      // (about 1 % on the step)
+      __builtin_amdgcn_s_setprio(1);
       bf16x8 vcur = tro.operand(tV, 0, 0);
 #pragma unroll
       for (int t = 0; t < 2 * kStepBlocks * DB; ++t) {
@@ -365,6 +368,7 @@ __global__ __launch_bounds__(256 * NG, 2) void attn_fwd_kernel(AttnArgs a, int k
         __builtin_amdgcn_sched_barrier(0);
         if (t + 1 < 2 * kStepBlocks * DB) vcur = vnext;
       }
+      __builtin_amdgcn_s_setprio(0);
     } else if (act_n) {
       scores(tKn, sn);
     }
