@@ -500,8 +500,32 @@ def layer_step_phase(torch, mga, syn, geo: dict, steps: int, warmup: int, seed: 
     a_pre, a_cur = tile_areas(bm, S, L, P)
     fl = Hq * D * (4 * (a_pre + a_cur) + 6 * a_pre + 10 * a_cur)
     tf = fl / (ms * 1e-3) / 1e12
+
+    # the three attention passes on their own (HIP events on the launch stream)
+    lib_ops = mga.ops
+    libc = importlib.import_module("mtp-glora_amd._lib")
+    kbuf, vbuf = cache.key_buffer(0), cache.value_buffer(0)
+    code, bmt = bm.mtp_code, bm.kernel_tensors()
+    kf, vf = kbuf[None, :, :L], vbuf[None, :, :L]
+    lib_ops.kv_append(k.detach(), v.detach(), kbuf, vbuf, dst_offset=P)
+    qd = q.detach()
+    o, lse = lib_ops.attn_fwd(qd, kf, vf, code, bmt, P, scale)
+    bufs = lib_ops.bwd_buffers(qd, kf, P)
+    timer = EventTimer(torch)
+    n = max(steps, 5)
+    t_fwd = timer(lambda: lib_ops.attn_fwd(qd, kf, vf, code, bmt, P, scale), n)
+    t_dq = timer(lambda: lib_ops.attn_bwd(qd, kf, vf, o, lse, do, code, bmt, P, scale, P,
+                                          passes=libc.BWD_DQ, buffers=bufs), n)
+    t_dkdv = timer(lambda: lib_ops.attn_bwd(qd, kf, vf, o, lse, do, code, bmt, P, scale, P,
+                                            passes=libc.BWD_DKDV, buffers=bufs), n)
+    passes = {}
+    for name, t, f in (("fwd", t_fwd, 4 * (a_pre + a_cur)), ("bwd_dq_pass", t_dq, 6 * (a_pre + a_cur)),
+                       ("bwd_dkdv_pass", t_dkdv, 4 * a_cur)):
+        pt = Hq * D * f / (t * 1e-3) / 1e12
+        passes[name] = {"ms": round(t, 4), "tflops": round(pt, 1), "frac": round(pt / PEAK_MFMA_BF16_TFLOPS, 4)}
     return {"chunk_rows": S, "prefix": P, "credited_gflop": round(fl / 1e9, 1), "ms_per_step": round(ms, 4),
-            "tflops": round(tf, 2), "frac": round(tf / PEAK_MFMA_BF16_TFLOPS, 4), "steps": steps}
+            "tflops": round(tf, 2), "frac": round(tf / PEAK_MFMA_BF16_TFLOPS, 4), "steps": steps,
+            "passes": passes}
 
 
 # config 3's last chunk: the north-star point
