@@ -60,34 +60,6 @@ __device__ __forceinline__ V rows16(const void *t, uint32_t ofs) {
 }
 typedef __attribute__((__vector_size__(16 * sizeof(uint32_t)))) uint32_t u32x16;
 
-// Raw buffer resource (stride 0) over nbytes from base: a load at a byte
-// offset >= nbytes returns zeros. base, nbytes are wave-uniform.
-__device__ __forceinline__ i32x4 buf_rsrc(const void *base, uint32_t nbytes) {
-  const uint64_t b = reinterpret_cast<uint64_t>(base);
-  i32x4 r;
-  r[0] = __builtin_amdgcn_readfirstlane((int)(uint32_t)b);
-  r[1] = __builtin_amdgcn_readfirstlane((int)((uint32_t)(b >> 32) & 0xffffu));
-  r[2] = __builtin_amdgcn_readfirstlane((int)nbytes);
-  r[3] = 0x00020000;
-  return r;
-}
-
-// Buffer -> LDS loads of 16 (or 4) bytes per lane: lane l writes LDS at
-// lds + 16 l (4 l), from byte offset voff of the resource. Inline asm outside
-// the compiler's wait counting: the caller owns the vmcnt waits.
-__device__ __forceinline__ void bdma16(const i32x4 &r, uint32_t voff, const void *lds) {
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
-               :
-               : "v"(voff), "s"(r), "s"(lds_addr(lds))
-               : "memory", "m0");
-}
-__device__ __forceinline__ void bdma4(const i32x4 &r, uint32_t voff, const void *lds) {
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dword %0, %1, 0 offen lds"
-               :
-               : "v"(voff), "s"(r), "s"(lds_addr(lds))
-               : "memory", "m0");
-}
-
 // The group's walk over its (query tile, head) pairs gr, gr + 2, ...: four
 // 32-row steps per pair, the step within the pair being the index of the
 // four-fold unrolled step loop. Advanced once per pair (no division).

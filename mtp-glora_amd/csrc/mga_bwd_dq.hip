@@ -129,27 +129,21 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnArgs a) {
   TrOffsets<HD> tro;
   tro.init(lane);
 
-  // K/V tiles go global -> LDS directly (no staging registers), addressed by
-  // a scalar row base plus precomputed 32-bit lane offsets
-  DmaLane<HD, kStep> dma;
-  dma.init();
-  const uint32_t lrowK = dma.lane_row(a.k_ss);
-  const uint32_t lrowV = dma.lane_row(a.v_ss);
-  const auto rowsK = dma.rows(a.k_ss);
-  const auto rowsV = dma.rows(a.v_ss);
+  // K/V tiles go global -> LDS directly (no staging registers) through
+  // buffer resources: precomputed lane offsets, the tile's first row in the
+  // resource base
+  BufDma<HD, kStep> dmaK, dmaV;
+  dmaK.init(a.k_ss);
+  dmaV.init(a.v_ss);
   KeyCode knext;
+  // rows past L arrive as zeros; a step past the keys is never computed
   auto load_step = [&](int j, bf16_t *dK, bf16_t *dV) {
     const int kb = step_base(j);
     const bf16_t *kr = reinterpret_cast<const bf16_t *>(kp) + (int64_t)kb * a.k_ss;
     const bf16_t *vr = reinterpret_cast<const bf16_t *>(vp) + (int64_t)kb * a.v_ss;
-    if (kb >= a.L) {
-      // a step past the keys is never computed: nothing to load
-    } else if (kb + kStep <= a.L) {
-      dma.issue(dK, kr, rowsK, lrowK);
-      dma.issue(dV, vr, rowsV, lrowV);
-    } else {
-      dma.issue_clamped(dK, kr, a.k_ss, a.L - kb);
-      dma.issue_clamped(dV, vr, a.v_ss, a.L - kb);
+    if (kb < a.L) {
+      dmaK.issue(dK, kr, a.k_ss, a.L - kb);
+      dmaV.issue(dV, vr, a.v_ss, a.L - kb);
     }
     if (tid < kStep) knext.load(a.code, kb + tid, a.P, a.L);   // converted at store time
   };

@@ -396,6 +396,34 @@ __device__ __forceinline__ void dma16(const void *gaddr, const void *lds) {
                : "memory", "m0");
 }
 
+// Raw buffer resource (stride 0) over nbytes from base: a load at a byte
+// offset >= nbytes returns zeros. base, nbytes are wave-uniform.
+__device__ __forceinline__ i32x4 buf_rsrc(const void *base, uint32_t nbytes) {
+  const uint64_t b = reinterpret_cast<uint64_t>(base);
+  i32x4 r;
+  r[0] = __builtin_amdgcn_readfirstlane((int)(uint32_t)b);
+  r[1] = __builtin_amdgcn_readfirstlane((int)((uint32_t)(b >> 32) & 0xffffu));
+  r[2] = __builtin_amdgcn_readfirstlane((int)nbytes);
+  r[3] = 0x00020000;
+  return r;
+}
+
+// Buffer -> LDS loads of 16 (or 4) bytes per lane: lane l writes LDS at
+// lds + 16 l (4 l), from byte offset voff of the resource. Inline asm outside
+// the compiler's wait counting: the caller owns the vmcnt waits.
+__device__ __forceinline__ void bdma16(const i32x4 &r, uint32_t voff, const void *lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+               :
+               : "v"(voff), "s"(r), "s"(lds_addr(lds))
+               : "memory", "m0");
+}
+__device__ __forceinline__ void bdma4(const i32x4 &r, uint32_t voff, const void *lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dword %0, %1, 0 offen lds"
+               :
+               : "v"(voff), "s"(r), "s"(lds_addr(lds))
+               : "memory", "m0");
+}
+
 // The wave's index within the workgroup as a scalar (wave-uniform) value, so
 // LDS block bases derived from it stay in scalar registers.
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
@@ -467,6 +495,41 @@ struct DmaLane {
       __builtin_amdgcn_global_load_lds(blk + vo, (lds_void *)(dst + i * 512), 16, 0, 0);
       blk += rs.inst;
     }
+  }
+};
+
+// The same tiles through a raw buffer resource whose range ends at the
+// source's last row: the lane offsets (row term for the source's stride plus
+// the swizzled granule) are formed once per source, the tile's first row goes
+// into the resource base, so a load costs no vector instruction, and rows at
+// or past the range's end arrive as zeros (no clamped form for a chunk's last
+// rows).
+template <int HD, int NR, int NW = 4>
+struct BufDma {
+  static constexpr int kGranRow = HD / 8;
+  static constexpr int kRowsPerInst = 64 / kGranRow;
+  static constexpr int kInst = NR / kRowsPerInst / NW;
+  static_assert(kInst >= 1 && kInst * kRowsPerInst * NW == NR, "tile rows must split evenly over the waves");
+  static_assert((NW & (NW - 1)) == 0, "NW must be a power of two");
+  __device__ __forceinline__ static int gw() { return wave_id() & (NW - 1); }
+  uint32_t vo[kInst];
+  __device__ __forceinline__ void init(int64_t ss) {
+    const int lane = threadIdx.x & 63, w = gw();
+    const int p = lane % kGranRow;
+#pragma unroll
+    for (int i = 0; i < kInst; ++i) {
+      const int r = (w * kInst + i) * kRowsPerInst + lane / kGranRow;
+      vo[i] = opaque_u32((uint32_t)(r * ss * 2) + (uint32_t)((p ^ swz<HD>(r)) << 4));
+    }
+  }
+  // rows 0 .. NR - 1 from rowbase (wave-uniform), the first nrows >= 1 of
+  // them in the source (the range: nrows rows of ss >= HD elements, so every
+  // 16-byte load of a row in range lies wholly inside it)
+  __device__ __forceinline__ void issue(bf16_t *tile, const void *rowbase, int64_t ss, int nrows) const {
+    const i32x4 r = buf_rsrc(rowbase, (uint32_t)((int64_t)min(nrows, NR) * ss * 2));
+    bf16_t *dst = tile + gw() * kInst * 512;
+#pragma unroll
+    for (int i = 0; i < kInst; ++i) bdma16(r, vo[i], dst + i * 512);
   }
 };
 

@@ -149,26 +149,19 @@ __global__ __launch_bounds__(256 * NG, 2) void attn_fwd_kernel(AttnArgs a, int k
       for (int mb = 0; mb < DB; ++mb) tro.off[sx][mb] = opaque_u32(tro.off[sx][mb] + gofs);
   }
 
-  DmaLane<HD, kStepKeys> dma;   // shared by the K and V tiles
-  dma.init();
-  const uint32_t lrowK = dma.lane_row(a.k_ss);
-  const uint32_t lrowV = dma.lane_row(a.v_ss);
-  const auto rowsK = dma.rows(a.k_ss);
-  const auto rowsV = dma.rows(a.v_ss);
+  BufDma<HD, kStepKeys> dmaK, dmaV;
+  dmaK.init(a.k_ss);
+  dmaV.init(a.v_ss);
   KeyCode wkey;
-  auto load_tile = [&](int kb, bf16_t *dst, const T *src, int64_t ss, const auto &rs, uint32_t lrow) {
-    if (kb >= a.L) {
-      // second half of the last tile, past the keys: never computed, nothing to load
-    } else if (kb + kStepKeys <= a.L) {
-      dma.issue(dst + grp * TILE, reinterpret_cast<const bf16_t *>(src) + (int64_t)kb * ss, rs, lrow);
-    } else {
-      dma.issue_clamped(dst + grp * TILE, reinterpret_cast<const bf16_t *>(src) + (int64_t)kb * ss, ss, a.L - kb);
-    }
+  // rows past L (the last tile's tail) arrive as zeros; a step that starts
+  // past L (the second half of the last tile) is never computed: no loads
+  auto load_tile = [&](int kb, bf16_t *dst, const T *src, int64_t ss, const BufDma<HD, kStepKeys> &d) {
+    if (kb < a.L) d.issue(dst + grp * TILE, reinterpret_cast<const bf16_t *>(src) + (int64_t)kb * ss, ss, a.L - kb);
   };
-  auto load_k = [&](int j, bf16_t *dK) { load_tile(step_base(j), dK, kp, a.k_ss, rowsK, lrowK); };
+  auto load_k = [&](int j, bf16_t *dK) { load_tile(step_base(j), dK, kp, a.k_ss, dmaK); };
   auto load_v = [&](int j, bf16_t *dV) {
     const int kb = step_base(j);
-    load_tile(kb, dV, vp, a.v_ss, rowsV, lrowV);
+    load_tile(kb, dV, vp, a.v_ss, dmaV);
     // raw code only: converting it here would wait for the tile loads too
     if (gtid < kStepKeys) wkey.load(a.code, kb + gtid, a.P, a.L);
   };
