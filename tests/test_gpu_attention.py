@@ -82,6 +82,9 @@ SMALL = [
     dict(n_reg=60, n_anchor=5, draft=2, P=0, Hq=4, Hkv=2, D=128, pad=3),        # S < 128
     dict(n_reg=200, n_anchor=20, draft=4, P=130, Hq=8, Hkv=1, D=128),           # G = 8: two head slices
     dict(n_reg=220, n_anchor=30, draft=3, P=70, Hq=8, Hkv=2, D=64, pad=9),      # G = 4 at head_dim 64
+    dict(n_reg=200, n_anchor=20, draft=4, P=150, Hq=7, Hkv=1, D=128),           # G = 7 (28 / 4 heads): one head per workgroup
+    dict(n_reg=180, n_anchor=15, draft=4, P=64, Hq=6, Hkv=2, D=128, pad=5),     # G = 3
+    dict(n_reg=160, n_anchor=12, draft=4, P=90, Hq=12, Hkv=2, D=64),            # G = 6: two heads per workgroup
 ]
 
 
