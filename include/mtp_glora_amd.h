@@ -113,6 +113,9 @@ int mga_mtp_block_mask(const int64_t *gate, int64_t gate_stride, int32_t S, int6
  * (o_sh = D, o_ss = Hq * D gives the [S, Hq, D] layout the attention wrapper returns).
  * Tiles are visited from the block-mask lists: empty tiles are skipped, partial
  * tiles evaluate the mask per element from `code`, full tiles do not.
+ * scale must be positive and finite (the models pass head_dim ** -0.5,
+ * modeling_qwen3.py:199); other values return MGA_ERR_INVALID, here and in
+ * the backward.
  * Replaces flex_attention_forward ([tf]integrations/flex_attention.py:262-368)
  * -> flex_attention ([torch]nn/attention/flex_attention.py:1396) as called from
  * modeling_qwen3.py:286-300 / modeling_llama.py:320-332.

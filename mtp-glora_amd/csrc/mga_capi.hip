@@ -73,8 +73,11 @@ int check_operand(const char *name, const void *p, int64_t sh, int64_t ss, int e
 }
 
 int check_attn_common(int32_t S, int32_t L, int32_t P, int32_t Hq, int32_t Hkv, int32_t hd,
-                      int32_t dtype) {
+                      int32_t dtype, float scale) {
   if (S <= 0) return fail(MGA_ERR_INVALID, "S must be positive (got %d)", S);
+  // the kernels mask a score to -inf before it is scaled
+  if (!(scale > 0.f) || !(scale < __builtin_huge_valf()))
+    return fail(MGA_ERR_INVALID, "scale must be positive and finite (got %g)", (double)scale);
   if (P < 0 || L != P + S) return fail(MGA_ERR_INVALID, "need L == P + S (L=%d P=%d S=%d)", L, P, S);
   if (Hq <= 0 || Hkv <= 0 || Hq % Hkv) return fail(MGA_ERR_INVALID, "Hq (%d) must be a positive multiple of Hkv (%d)", Hq, Hkv);
   if (hd != 64 && hd != 128) return fail(MGA_ERR_INVALID, "head_dim must be 64 or 128 (got %d)", hd);
@@ -185,7 +188,7 @@ int mga_attn_fwd(const void *q, int64_t q_sh, int64_t q_ss, const void *k, int64
                  int32_t S, int32_t L, int32_t P, int32_t Hq, int32_t Hkv, int32_t head_dim,
                  int32_t dtype, float scale, void *stream) {
   int rc;
-  if ((rc = check_attn_common(S, L, P, Hq, Hkv, head_dim, dtype))) return rc;
+  if ((rc = check_attn_common(S, L, P, Hq, Hkv, head_dim, dtype, scale))) return rc;
   const int eb = elem_bytes(dtype);
   if ((rc = check_operand("q", q, q_sh, q_ss, eb))) return rc;
   if ((rc = check_operand("k", k, k_sh, k_ss, eb))) return rc;
@@ -221,7 +224,7 @@ int mga_attn_bwd(const void *q, int64_t q_sh, int64_t q_ss, const void *k, int64
                  int32_t Hkv, int32_t head_dim, int32_t dtype, float scale, int32_t passes,
                  void *stream) {
   int rc;
-  if ((rc = check_attn_common(S, L, P, Hq, Hkv, head_dim, dtype))) return rc;
+  if ((rc = check_attn_common(S, L, P, Hq, Hkv, head_dim, dtype, scale))) return rc;
   if (passes <= 0 || (passes & ~(MGA_BWD_DQ | MGA_BWD_DKDV)))
     return fail(MGA_ERR_INVALID, "mga_attn_bwd: passes must be a non-empty set of MGA_BWD_DQ | MGA_BWD_DKDV (got %d)", passes);
   const int eb = elem_bytes(dtype);

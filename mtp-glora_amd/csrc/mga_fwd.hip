@@ -220,19 +220,11 @@ __global__ __launch_bounds__(256 * NG, 2) void attn_fwd_kernel(AttnArgs a, int k
       for (int kb = 0; kb < kStepBlocks; ++kb) s[kb] = mfma32<E>(ka[kb], qf[ks], s[kb]);
     }
   };
-  // Scores are shifted in place, t = s * c - m_eff (m_eff: the running offset,
-  // 0 while it is still -inf), so the raw scores die there; the slow path
-  // works from t too. probs(t, d) = exp2(t + d) packed as O^T's B operands
-  // (d only on the slow path); returns the lane's partial row sum.
-  auto shift = [&](f32x16 (&s)[kStepBlocks], float m_eff) {
-#pragma unroll
-    for (int kb = 0; kb < kStepBlocks; ++kb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) s[kb][r] = __builtin_fmaf(s[kb][r], c, -m_eff);
-  };
+  // probs(s, m) = exp2(s * c - m) (one fma per score, inside the exponent's
+  // operand) packed as O^T's B operands; returns the lane's partial row sum.
+  // The raw scores stay in s: the slow path reads them again.
   bf16x8 pb[2 * kStepBlocks];
-  auto probs = [&](auto shifted, const f32x16 (&t)[kStepBlocks], float d) {
-    constexpr bool SHIFTED = decltype(shifted)::value;
+  auto probs = [&](const f32x16 (&s)[kStepBlocks], float m) {
     float ps = 0.f;
 #pragma unroll
     for (int kb = 0; kb < kStepBlocks; ++kb)
@@ -241,12 +233,8 @@ __global__ __launch_bounds__(256 * NG, 2) void attn_fwd_kernel(AttnArgs a, int k
         i32x4 wv;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          float x0 = t[kb][8 * u + 2 * q], x1 = t[kb][8 * u + 2 * q + 1];
-          if constexpr (SHIFTED) {
-            x0 += d;
-            x1 += d;
-          }
-          const float e0 = exp2f_(x0), e1 = exp2f_(x1);
+          const float e0 = exp2f_(__builtin_fmaf(s[kb][8 * u + 2 * q], c, -m));
+          const float e1 = exp2f_(__builtin_fmaf(s[kb][8 * u + 2 * q + 1], c, -m));
           wv[q] = (int)cvt2<E>(e0, e1);
           ps += e0 + e1;
         }
@@ -255,9 +243,9 @@ __global__ __launch_bounds__(256 * NG, 2) void attn_fwd_kernel(AttnArgs a, int k
     return ps;
   };
   // the interleave of a fused region: K reads, MFMAs and the VALU work of
-  // shift + probs (32 fma + 32 exp2 + 16 cvt + 32 adds per step)
+  // probs (32 fma + 32 exp2 + 16 cvt + 32 adds per step)
   auto interleave = [&]() {
-    constexpr int kValuPer = 96 / (KS * kStepBlocks);
+    constexpr int kValuPer = 112 / (KS * kStepBlocks);
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       __builtin_amdgcn_sched_group_barrier(kSgDsRead, kStepBlocks, 0);
@@ -316,14 +304,17 @@ __global__ __launch_bounds__(256 * NG, 2) void attn_fwd_kernel(AttnArgs a, int k
       const float m_eff = m_run == kNegInfF ? 0.f : m_run;
       float ps;
       if (act_n) {
-        // one region: step j + 1's MFMAs interleaved with step j's softmax
+        // one region: step j + 1's MFMAs interleaved with step j's softmax.
+        // The offset passes through an empty asm so that this region's fmas
+        // differ from the other branch's and stay here instead of being
+        // hoisted above the branch, out of reach of the interleave.
+        float mf = m_eff;
+        asm volatile("" : "+v"(mf));
         scores_fused(tKn, sn);
-        shift(s, m_eff);
-        ps = probs(std::false_type{}, s, 0.f);
+        ps = probs(s, mf);
         interleave();
       } else {
-        shift(s, m_eff);
-        ps = probs(std::false_type{}, s, 0.f);
+        ps = probs(s, m_eff);
       }
       // slow path: no offset yet, or a partial row sum past the bound
       if (__builtin_amdgcn_ballot_w64(!(ps <= kPBound<E>) | (m_run == kNegInfF))) {
@@ -332,7 +323,7 @@ __global__ __launch_bounds__(256 * NG, 2) void attn_fwd_kernel(AttnArgs a, int k
         for (int kb = 0; kb < kStepBlocks; ++kb)
 #pragma unroll
           for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
-        mx = fmaxf(mx, xor32(mx)) + m_eff;   // the row's max of s * c
+        mx = fmaxf(mx, xor32(mx)) * c;   // the row's max of s * c (c > 0)
         const float m_new = fmaxf(m_run, mx);
         if (m_new > m_run) {
           const float alpha = exp2f_(m_run - m_new);   // 0 when m_run = -inf
@@ -343,7 +334,7 @@ __global__ __launch_bounds__(256 * NG, 2) void attn_fwd_kernel(AttnArgs a, int k
             for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
           m_run = m_new;
         }
-        ps = probs(std::true_type{}, s, m_eff - (m_run == kNegInfF ? 0.f : m_run));
+        ps = probs(s, m_run == kNegInfF ? 0.f : m_run);
       }
       l_run += ps;
       // O^T += V^T P^T; operand t = (16-key slice t / DB, output block t % DB),

@@ -78,6 +78,10 @@ def test_attention_invalid_arguments(mga):
     # unsupported head_dim
     rc = lib.mga_attn_fwd(*base, 100, 110, 10, 32, 8, 96, 0, 0.1, None)
     assert rc == mga._lib.MGA_ERR_INVALID and b"head_dim" in lib.mga_last_error()
+    # the kernels take a positive, finite scale (the reference's head_dim ** -0.5)
+    for bad in (0.0, -0.1, float("inf"), float("nan")):
+        rc = lib.mga_attn_fwd(*base, 100, 110, 10, 32, 8, 128, 0, bad, None)
+        assert rc == mga._lib.MGA_ERR_INVALID and b"scale" in lib.mga_last_error()
 
 
 def test_python_errors_are_raised(mga):
