@@ -62,8 +62,7 @@ __device__ __forceinline__ float half_row_dot(const T *o, const T *d, int hi) {
 }  // namespace
 
 template <int HD, typename T, int MODE>
-__global__ __launch_bounds__(MODE == kDq4 ? 256 : 512, MODE == kDq4 ? 2 : 1) void attn_bwd_dq_kernel(AttnArgs a, int k1,
-                                                                                                   int kn) {
+__global__ __launch_bounds__(MODE == kDq4 ? 256 : 512, 2) void attn_bwd_dq_kernel(AttnArgs a, int k1, int kn) {
   constexpr int NG = MODE == kDqSplit ? 2 : 1;    // groups splitting the tile list
   constexpr int NWD = MODE == kDqPair ? 8 : 4;    // waves sharing each staged tile
   typedef typename MfmaElem<T>::type E;
