@@ -185,11 +185,13 @@ __global__ __launch_bounds__(MODE == kDq4 ? 256 : 512, 2) void attn_bwd_dq_kerne
     const int kb = step_base(j);
     const bf16_t *kr = reinterpret_cast<const bf16_t *>(kp) + (int64_t)kb * a.k_ss;
     const bf16_t *vr = reinterpret_cast<const bf16_t *>(vp) + (int64_t)kb * a.v_ss;
+    // the code read first: the compiler, which does not see the tile loads,
+    // waits for every outstanding load before it writes the code register
+    if (gtid < kStep) knext.load(a.code, kb + gtid, a.P, a.L);   // converted at store time
     if (kb < a.L) {
       dmaK.issue(dK + grp * TILE, kr, a.k_ss, a.L - kb);
       dmaV.issue(dV + grp * TILE, vr, a.v_ss, a.L - kb);
     }
-    if (gtid < kStep) knext.load(a.code, kb + gtid, a.P, a.L);   // converted at store time
   };
   auto store_step = [&](bf16_t *, bf16_t *, int *dW) {
     __builtin_amdgcn_s_waitcnt(0);   // this thread's direct loads have landed

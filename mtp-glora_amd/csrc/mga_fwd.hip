@@ -159,12 +159,14 @@ __global__ __launch_bounds__(256 * NG, 2) void attn_fwd_kernel(AttnArgs a, int k
     if (kb < a.L) d.issue(dst + grp * TILE, reinterpret_cast<const bf16_t *>(src) + (int64_t)kb * ss, ss, a.L - kb);
   };
   auto load_k = [&](int j, bf16_t *dK) { load_tile(step_base(j), dK, kp, a.k_ss, dmaK); };
-  auto load_v = [&](int j, bf16_t *dV) {
-    const int kb = step_base(j);
-    load_tile(kb, dV, vp, a.v_ss, dmaV);
-    // raw code only: converting it here would wait for the tile loads too
-    if (gtid < kStepKeys) wkey.load(a.code, kb + gtid, a.P, a.L);
+  // the keys' raw codes of step j, read before any tile load of the step:
+  // the compiler, which does not see the tile loads, waits for every
+  // outstanding load before it writes the code register (and converting the
+  // code here would wait for the read)
+  auto load_w = [&](int j) {
+    if (gtid < kStepKeys) wkey.load(a.code, step_base(j) + gtid, a.P, a.L);
   };
+  auto load_v = [&](int j, bf16_t *dV) { load_tile(step_base(j), dV, vp, a.v_ss, dmaV); };
   auto store_w = [&](int *dW) {
     if (gtid < kStepKeys)
       *reinterpret_cast<int *>(const_cast<char *>(lds_at(dW + grp * kStepKeys, opaque_u32(gtid * 4u)))) = wkey.w();
@@ -270,6 +272,7 @@ __global__ __launch_bounds__(256 * NG, 2) void attn_fwd_kernel(AttnArgs a, int k
     const bool act = kbase < a.L;
     const bool act_n = j + 1 < nstep && step_base(j + 1) < a.L;
     const bool partial = tile_of(j) < npart;
+    if (j + 1 < nstep) load_w(j + 1);
     if (j + 2 < nstep) load_k(j + 2, B ? sK1 : sK0);
     if (j + 1 < nstep) load_v(j + 1, B ? sV0 : sV1);
 
@@ -366,6 +369,7 @@ __global__ __launch_bounds__(256 * NG, 2) void attn_fwd_kernel(AttnArgs a, int k
 
   // prologue: K and V of step 0, K of step 1; the scores of step 0
   if (nstep > 0) {
+    load_w(0);
     load_k(0, sK0);
     load_v(0, sV0);
     if (nstep > 1) load_k(1, sK1);
