@@ -106,9 +106,9 @@ def test_attention_small_fp16(mga, dev, c):
 
 
 # Keys of at least 16 tiles and at most one round of items per XCD: the
-# forward runs every item as a two-group workgroup (even and odd tiles of the
-# item's list, merged through LDS). Configs 2 and 4 run the mixed launch (the
-# last round two-group) in test_attention_full_config.
+# forward and the dQ pass run every item as two-group workgroups (even and
+# odd tiles of the item's list, merged through LDS). Configs 2 and 4 run the
+# mixed launches (the last round two-group) in test_attention_full_config.
 SPLIT = [
     dict(n_reg=800, n_anchor=50, draft=4, P=1536, Hq=8, Hkv=2, D=128, pad=11),
     dict(n_reg=700, n_anchor=60, draft=4, P=1800, Hq=4, Hkv=1, D=64, tail=True),

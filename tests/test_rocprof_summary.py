@@ -77,3 +77,9 @@ def test_kernel_labels_tell_the_forward_forms_apart():
     assert rs.kernel_label("void mga::attn_fwd_kernel<128, __bf16, 2>(mga::AttnArgs, int, int)") == \
         "attn_fwd_kernel (two-group)"
     assert rs.kernel_label("_ZN3mga18attn_bwd_dq_kernelILi128EDF16bEEvNS_8AttnArgsE") == "attn_bwd_dq_kernel"
+    assert rs.kernel_label("_ZN3mga18attn_bwd_dq_kernelILi128EDF16bLi1EEEvNS_8AttnArgsEii") == \
+        "attn_bwd_dq_kernel (8-wave pair)"
+    assert rs.kernel_label("_ZN3mga18attn_bwd_dq_kernelILi64EDF16_Li2EEEvNS_8AttnArgsEii") == \
+        "attn_bwd_dq_kernel (two-group)"
+    assert rs.kernel_label("void mga::attn_bwd_dq_kernel<128, __bf16, 0>(mga::AttnArgs, int, int)") == \
+        "attn_bwd_dq_kernel (4-wave)"
