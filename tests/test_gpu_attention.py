@@ -241,6 +241,17 @@ def test_attention_full_config(mga, dev, cfg):
     full_config_case(mga, dev, cfg, torch.bfloat16)
 
 
+# Config 2's chunk and prefix with other head geometries, each launching the
+# dQ pass as 8-wave pair items plus a two-group last round: G = 2 (two heads
+# per slice, 128 rows per item: 320 items), G = 8 (two slices of four heads:
+# 640 items) and D = 64.
+@pytest.mark.parametrize("heads", [dict(Hq=16, Hkv=8, D=128), dict(Hq=32, Hkv=4, D=128),
+                                   dict(Hq=32, Hkv=8, D=64)],
+                         ids=lambda h: f"hq{h['Hq']}_hkv{h['Hkv']}_d{h['D']}")
+def test_attention_config2_head_geometries(mga, dev, heads):
+    full_config_case(mga, dev, dict(n_reg=4096, n_anchor=256, draft=4, P=8192, **heads), torch.bfloat16)
+
+
 def test_attention_full_config_fp16(mga, dev):
     """Config 2's geometry with fp16 operands, fp16 bounds."""
     full_config_case(mga, dev, dict(n_reg=4096, n_anchor=256, draft=4, P=8192), torch.float16,
@@ -255,7 +266,7 @@ def test_attention_full_config_fp32(mga, dev):
 
 
 def full_config_case(mga, dev, cfg, dtype, max_abs=MAX_ABS, mean_abs=MEAN_ABS, grad_scaled=False):
-    Hq, Hkv, D = 32, 8, 128
+    Hq, Hkv, D = cfg.get("Hq", 32), cfg.get("Hkv", 8), cfg.get("D", 128)
     seq, q, k, v, kp, vp, do, o, lse = run_case(
         mga, dev, cfg["n_reg"], cfg["n_anchor"], cfg["draft"], cfg["P"], Hq, Hkv, D, seed=2,
         every=cfg.get("every"), dtype=dtype)
