@@ -19,12 +19,17 @@
   figures for the attention kernels: MFMA busy fraction (busy cycles of the
   MFMA units over all SIMDs' active cycles), the bf16 MFMA work the counters
   count against the credited work, and instructions per MFMA.
+* ``clock``: one run with ``--pmc GRBM_GUI_ACTIVE --kernel-trace``: each
+  dispatch's average clock, its GPU-active cycles per XCD
+  (``GRBM_GUI_ACTIVE`` summed over the 8 XCDs, / 8) over its traced
+  duration, median per attention kernel.
 
     python mtp-glora_amd/rocprof_summary.py stats TRACE_DIR/bench_kernel_stats.csv
     python mtp-glora_amd/rocprof_summary.py traffic --fetch F.csv --write W.csv \\
         --calib-read BYTES --calib-write BYTES --config 2 -o profiles/config2_traffic.json
     python mtp-glora_amd/rocprof_summary.py mfma --pass-json PASS.json A.csv B.csv \\
         -o profiles/config2_mfma.json
+    python mtp-glora_amd/rocprof_summary.py clock COUNTERS.csv KERNEL_TRACE.csv
 """
 from __future__ import annotations
 
@@ -184,6 +189,35 @@ def mfma_summary(paths, credited: dict) -> dict:
     return res
 
 
+def kernel_clocks(counter_csv: str, trace_csv: str, xcds: int = 8) -> dict:
+    """Median clock (GHz) and duration (us) per attention kernel: per
+    dispatch, GRBM_GUI_ACTIVE (summed over the XCDs) / xcds cycles over the
+    traced end - start nanoseconds."""
+    cyc = {}
+    for r in csv.DictReader(open(counter_csv)):
+        if r["Counter_Name"] == "GRBM_GUI_ACTIVE":
+            cyc[r["Dispatch_Id"]] = cyc.get(r["Dispatch_Id"], 0.0) + float(r["Counter_Value"])
+    per = {}
+    for r in csv.DictReader(open(trace_csv)):
+        d = r["Dispatch_Id"]
+        if d not in cyc:
+            continue
+        k = kernel_base(r["Kernel_Name"])
+        if k not in ATTN_KERNELS:
+            continue
+        ns = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+        if ns > 0:
+            per.setdefault(k, []).append((cyc[d] / xcds / ns, ns / 1e3))
+    out = {}
+    for k, v in per.items():
+        ghz = sorted(x[0] for x in v)
+        us = sorted(x[1] for x in v)
+        out[k] = {"dispatches": len(v), "median_ghz": round(ghz[len(ghz) // 2], 3),
+                  "min_ghz": round(ghz[0], 3), "max_ghz": round(ghz[-1], 3),
+                  "median_us": round(us[len(us) // 2], 1)}
+    return out
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     sub = ap.add_subparsers(dest="cmd", required=True)
@@ -200,6 +234,10 @@ def main(argv=None) -> int:
     m.add_argument("csvs", nargs="+")
     m.add_argument("--pass-json", help="the JSON line bench.py --pmc-pass printed (credited FLOPs)")
     m.add_argument("-o", "--out")
+    c = sub.add_parser("clock")
+    c.add_argument("counters")
+    c.add_argument("trace")
+    c.add_argument("-o", "--out")
     args = ap.parse_args(argv)
     if args.cmd == "stats":
         print(stats_markdown(args.csv))
@@ -212,6 +250,8 @@ def main(argv=None) -> int:
                 if line.startswith("{") and "pmc_pass" in line:
                     credited = json.loads(line).get("credited_flop", {})
         res = mfma_summary(args.csvs, credited)
+    elif args.cmd == "clock":
+        res = kernel_clocks(args.counters, args.trace)
     else:
         res = traffic(args.fetch, args.write, args.calib_read, args.calib_write, args.config)
     text = json.dumps(res, indent=1)

@@ -83,3 +83,30 @@ def test_kernel_labels_tell_the_forward_forms_apart():
         "attn_bwd_dq_kernel (two-group)"
     assert rs.kernel_label("void mga::attn_bwd_dq_kernel<128, __bf16, 0>(mga::AttnArgs, int, int)") == \
         "attn_bwd_dq_kernel (4-wave)"
+
+
+def test_kernel_clocks_from_gui_active_over_duration(tmp_path):
+    """Clock = GRBM_GUI_ACTIVE summed over 8 XCDs / 8 over the traced
+    duration; dispatches without the counter and other kernels are left out."""
+    c, t = tmp_path / "c.csv", tmp_path / "t.csv"
+    dq = "_ZN3mga18attn_bwd_dq_kernelILi128EDF16bLi1EEEvNS_8AttnArgsEii"
+    with open(c, "w", newline="") as fh:
+        wr = csv.DictWriter(fh, fieldnames=FIELDS)
+        wr.writeheader()
+        # 8 XCDs x 250 000 cycles over 100 us: 2.5 GHz; 8 x 200 000 over 100 us: 2.0 GHz
+        for d, v in ((1, 250000.0), (2, 200000.0), (3, 200000.0)):
+            for x in range(8):
+                wr.writerow(dict(Dispatch_Id=d, Grid_Size=1, Kernel_Name=dq, Counter_Name="GRBM_GUI_ACTIVE",
+                                 Counter_Value=v))
+    with open(t, "w", newline="") as fh:
+        wr = csv.DictWriter(fh, fieldnames=["Dispatch_Id", "Kernel_Name", "Start_Timestamp", "End_Timestamp"])
+        wr.writeheader()
+        wr.writerow(dict(Dispatch_Id=1, Kernel_Name=dq, Start_Timestamp=0, End_Timestamp=100000))
+        wr.writerow(dict(Dispatch_Id=2, Kernel_Name=dq, Start_Timestamp=0, End_Timestamp=100000))
+        wr.writerow(dict(Dispatch_Id=3, Kernel_Name="kv_copy_rows_kernel", Start_Timestamp=0, End_Timestamp=1000))
+        wr.writerow(dict(Dispatch_Id=4, Kernel_Name=dq, Start_Timestamp=0, End_Timestamp=5000))
+    r = rs.kernel_clocks(str(c), str(t))
+    assert list(r) == ["attn_bwd_dq_kernel"]
+    assert r["attn_bwd_dq_kernel"]["dispatches"] == 2
+    assert r["attn_bwd_dq_kernel"]["min_ghz"] == 2.0 and r["attn_bwd_dq_kernel"]["max_ghz"] == 2.5
+    assert r["attn_bwd_dq_kernel"]["median_us"] == 100.0
