@@ -935,7 +935,7 @@ def main() -> int:
     if args.north_star_steps > 0:
         out["north_star"] = north_star_phase(torch, mga, syn, args.north_star_steps, 3)
     if args.extra and args.config == 2:
-        # the other workloads BASELINE.md quotes, measured in the same run
+        # config 3's whole stream and config 5's step, measured in the same run
         st = STREAMS[3]
         m = stream_measure(torch, mga, syn, st)
         out["config3_stream"] = {"workload": st["workload"], "credited_tflop": round(m["credited"] / 1e12, 2),

@@ -155,7 +155,7 @@ def test_last_bucket():
     assert mo.pick_last_bucket(4100, 4500, 1024) == 4500
 
 
-def test_credited_flops_match_survey_figures():
+def test_credited_flops_match_published_figures():
     """Config 2 (S=5120, P=8192) and config 5 (S=6144, P=16384) credited work:
     907.3 / 1581.1 GFLOP and 1964.9 / 3263.1 GFLOP (fwd / bwd) per layer."""
     seq = mo.synth_sequence(4096, mo.sample_anchors(4096, 256, 0), 4, pos0=8192)
