@@ -757,6 +757,8 @@ def main() -> int:
                     help="counter summary (rocprof_summary.py mfma) that fills roofline.mfma_busy")
     ap.add_argument("--north-star-steps", type=int, default=10,
                     help="timed steps of the north-star point (0 = skip)")
+    ap.add_argument("--north-star-only", action="store_true",
+                    help="time the north-star point alone (for a kernel trace of that workload)")
     ap.add_argument("--extra", type=int, default=1,
                     help="also time the config-3 stream (36 layers x 8 chunks) and the config-5 step (0 = skip)")
     args = ap.parse_args()
@@ -782,6 +784,9 @@ def main() -> int:
 
     if args.config in STREAMS:
         return stream_bench(torch, mga, syn, args.config, STREAMS[args.config], args.cpu_reps)
+    if args.north_star_only:
+        print(json.dumps({"north_star": north_star_phase(torch, mga, syn, max(args.north_star_steps, 1), 3)}))
+        return 0
 
     cfg = CONFIGS[args.config]
     Hq, Hkv, D, P = cfg["Hq"], cfg["Hkv"], cfg["D"], cfg["P"]
