@@ -16,9 +16,9 @@
 //   two workgroups per CU.
 // Each XCD (workgroup id mod 8) runs a contiguous share of the kDqPair items,
 // kv head major and longest first, so the tail round holds the shortest.
-// Q and dO stay in registers. K/V tiles are staged
-// 64 keys at a time (one barrier and one set of direct loads per step); per
-// 32-key block of a step each wave computes
+// Q and dO stay in registers. K/V tiles are staged 64 keys at a time (one
+// barrier and one set of direct loads per step); per 32-key block of a step
+// each wave computes
 //   S^T  = K Q^T,  dP^T = V dO^T                    (A operands: K, V rows)
 //   P    = exp2(S^T * scale_log2 - lse_log2)         (0 where masked)
 //   dS^T = P (dP^T - delta)
