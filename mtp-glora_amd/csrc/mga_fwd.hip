@@ -62,16 +62,35 @@ __device__ __forceinline__ float exp2f_(float x) { return __builtin_amdgcn_exp2f
 
 // Heads sharing a workgroup (a divisor of both G and 4).
 __host__ __device__ __forceinline__ int heads_per_wg(int G) { return (G % 4 == 0) ? 4 : (G % 2 == 0 ? 2 : 1); }
+// Row blocks of 4 waves per item: 2 when the heads split into slices of 2 or
+// 4 (an item's rows then still lie in one 128-row query tile), else 1.
+__host__ __device__ __forceinline__ int units_per_item(int HPW) { return HPW >= 2 ? 2 : 1; }
+
+enum { kFwd4 = 0, kFwdPair = 1, kFwdSplit = 2 };
 
 }  // namespace
 
-// NG = 1: 4 waves per workgroup, one item each. NG = 2: 8 waves, two 4-wave
-// groups taking the even and the odd entries of one item's tile list and
-// merging (O, offset, row sum) through LDS at the end, so an item takes
-// about half as long (for a last round of workgroups that would leave half
-// the GPU idle). The launch runs items [k1, k1 + kn) of each XCD's share.
-template <int HD, typename T, int NG>
-__global__ __launch_bounds__(256 * NG, 2) void attn_fwd_kernel(AttnArgs a, int k1, int kn) {
+// An item is (kv head, slice of HPW query heads, U consecutive blocks of
+// 4 * 32 / HPW rows), U = units_per_item; a wave holds one (query head,
+// 32-row block) pair. Forms:
+// * kFwdPair (U = 2): 8 waves, one workgroup per CU; each staged K/V tile
+//   feeds all 8 waves (half the tile loads and LDS writes per MFMA of two
+//   4-wave workgroups sharing the CU). A step runs as two barrier intervals,
+//   the scores and softmax (F) and the O^T update (P), and the second row
+//   block (waves 4-7, each sharing a SIMD with one of waves 0-3) runs one
+//   interval behind the first: each SIMD holds one wave in its softmax while
+//   the other multiplies, instead of two waves held in the same phase.
+// * kFwd4 (U = 1): 4 waves, two workgroups per CU.
+// * kFwdSplit: each row block of an item as an 8-wave workgroup whose two
+//   4-wave groups take the even and the odd entries of the tile list and
+//   merge (O, offset, row sum) through LDS at the end, so the block takes
+//   about half as long (for a last round of workgroups that would leave half
+//   the GPU idle).
+// The launch runs items [k1, k1 + kn) of each XCD's share.
+template <int HD, typename T, int MODE>
+__global__ __launch_bounds__(MODE == kFwd4 ? 256 : 512, 2) void attn_fwd_kernel(AttnArgs a, int k1, int kn) {
+  constexpr int NG = MODE == kFwdSplit ? 2 : 1;    // groups splitting the tile list
+  constexpr int NWD = 4;                           // waves loading each staged tile
   typedef typename MfmaElem<T>::type E;
   constexpr int KS = HD / 16;          // k-steps of QK^T over head_dim
   constexpr int DB = HD / 32;          // 32-dim blocks of O^T
@@ -82,24 +101,28 @@ __global__ __launch_bounds__(256 * NG, 2) void attn_fwd_kernel(AttnArgs a, int k
   __shared__ __attribute__((aligned(16))) int sW0[NG * kStepKeys], sW1[NG * kStepKeys];
 
   const int tid = threadIdx.x, lane = tid & 63;
-  const int grp = NG == 2 ? wave_id() >> 2 : 0;   // the group's entries: grp, grp + NG, ...
-  const int wave = wave_id() & 3;                 // wave within the group
-  const int gtid = tid & 255;
+  const int grp = NG == 2 ? wave_id() >> 2 : 0;                // the group's entries: grp, grp + NG, ...
+  const int wave = NG == 2 ? wave_id() & 3 : wave_id();        // wave among those holding the rows
+  const int gtid = NG == 2 ? tid & 255 : tid;
   const int l32 = lane & 31, hi = lane >> 5;
   const int G = a.Hq / a.Hkv;
   const int HPW = heads_per_wg(G);
-  const int QR = 32 * (4 / HPW);          // query rows per workgroup (<= 128)
+  const int QR4 = 32 * (4 / HPW);         // rows of 4 waves (<= 128)
+  const int U = units_per_item(HPW);
+  const int QU = U * QR4;                 // rows of an item (<= 128)
   const int nslice = G / HPW;
-  const int nqb = (a.S + QR - 1) / QR;
+  const int nqb = (a.S + QU - 1) / QU;
 
   // logical item: kv head major (one kv head per XCD when Hkv = 8), then query
   // blocks from the last (longest) to the first, then the head slice
   // item: XCD x = blockIdx % 8 runs the contiguous share x0 .. x0 + n_x - 1
   // of the logical items (kv head major, longest first), this launch its
   // entries k1 .. k1 + kn - 1
+  // (a kFwdSplit workgroup: entry t / U, row block t % U of it)
   const int n_items = a.Hkv * nslice * nqb;
   const int xcd = blockIdx.x & 7;
-  const int o = k1 + (int)(blockIdx.x >> 3);
+  const int t = (int)(blockIdx.x >> 3);
+  const int o = k1 + (MODE == kFwdSplit ? t / U : t);
   const int n_x = n_items / 8 + (xcd < n_items % 8 ? 1 : 0);
   if (o >= n_x || o >= k1 + kn) return;
   const int li = xcd * (n_items / 8) + min(xcd, n_items % 8) + o;
@@ -107,9 +130,10 @@ __global__ __launch_bounds__(256 * NG, 2) void attn_fwd_kernel(AttnArgs a, int k
   const int rem = li % (nslice * nqb);
   const int qb = nqb - 1 - rem / nslice;
   const int slice = rem % nslice;
+  const int wg_row0 = qb * QU + (MODE == kFwdSplit ? (t % U) * QR4 : 0);
   const int h = g * G + slice * HPW + wave % HPW;
-  const int row0 = qb * QR + (wave / HPW) * 32;        // first row of this wave
-  const int qt = (qb * QR) / kBlock;                   // block-mask query tile
+  const int row0 = wg_row0 + (wave / HPW) * 32;        // first row of this wave
+  const int qt = wg_row0 / kBlock;                     // block-mask query tile
 
   const T *qp = reinterpret_cast<const T *>(a.q) + h * a.q_sh;
   const T *kp = reinterpret_cast<const T *>(a.k) + g * a.k_sh;
@@ -149,13 +173,16 @@ __global__ __launch_bounds__(256 * NG, 2) void attn_fwd_kernel(AttnArgs a, int k
       for (int mb = 0; mb < DB; ++mb) tro.off[sx][mb] = opaque_u32(tro.off[sx][mb] + gofs);
   }
 
-  BufDma<HD, kStepKeys> dmaK, dmaV;
-  dmaK.init(a.k_ss);
-  dmaV.init(a.v_ss);
+  // (kFwdPair: waves 0-3 load only K, waves 4-7 only V, so each wave keeps
+  // the lane offsets of one tile kind: dmaV is dmaK, set up with V's stride)
+  BufDma<HD, kStepKeys, NWD> dmaK, dmaV_own;
+  dmaK.init(MODE == kFwdPair && wave_id() >= 4 ? a.v_ss : a.k_ss);
+  if constexpr (MODE != kFwdPair) dmaV_own.init(a.v_ss);
+  const BufDma<HD, kStepKeys, NWD> &dmaV = MODE == kFwdPair ? dmaK : dmaV_own;
   KeyCode wkey;
   // rows past L (the last tile's tail) arrive as zeros; a step that starts
   // past L (the second half of the last tile) is never computed: no loads
-  auto load_tile = [&](int kb, bf16_t *dst, const T *src, int64_t ss, const BufDma<HD, kStepKeys> &d) {
+  auto load_tile = [&](int kb, bf16_t *dst, const T *src, int64_t ss, const BufDma<HD, kStepKeys, NWD> &d) {
     if (kb < a.L) d.issue(dst + grp * TILE, reinterpret_cast<const bf16_t *>(src) + (int64_t)kb * ss, ss, a.L - kb);
   };
   auto load_k = [&](int j, bf16_t *dK) { load_tile(step_base(j), dK, kp, a.k_ss, dmaK); };
@@ -260,22 +287,40 @@ __global__ __launch_bounds__(256 * NG, 2) void attn_fwd_kernel(AttnArgs a, int k
     }
   };
 
-  // step j (parity B): softmax and O^T of step j, scores of step j + 1
-  auto run_step = [&](auto bsel, int j) {
+  // F(j), step j of parity B: the softmax of step j with the scores of step
+  // j + 1 (past the group's steps: nothing)
+  // O^T += V^T P^T of the step whose V is in tV; operand t = (16-key slice
+  // t / DB, output block t % DB), read one ahead. The wave issues at raised
+  // priority meanwhile, so the SIMD's other wave, usually in its softmax,
+  // yields it the issue slots (about 1 % on the step)
+  auto pv = [&](const bf16_t *tV) __attribute__((always_inline)) {
+    __builtin_amdgcn_s_setprio(1);
+    bf16x8 vcur = tro.operand(tV, 0, 0);
+#pragma unroll
+    for (int t = 0; t < 2 * kStepBlocks * DB; ++t) {
+      bf16x8 vnext;
+      if (t + 1 < 2 * kStepBlocks * DB) vnext = tro.operand(tV, ((t + 1) / DB) * 16, (t + 1) % DB);
+      __builtin_amdgcn_sched_barrier(0);
+      oacc[t % DB] = mfma32<E>(vcur, pb[t / DB], oacc[t % DB]);
+      __builtin_amdgcn_sched_barrier(0);
+      if (t + 1 < 2 * kStepBlocks * DB) vcur = vnext;
+    }
+    __builtin_amdgcn_s_setprio(0);
+  };
+  // (WP: followed by the O^T update of step j, in the same branch; FZ: with
+  // the scores of step j + 1, else the softmax alone)
+  auto fphase = [&](auto bsel, auto wp_sel, auto fz_sel, int j) __attribute__((always_inline)) {
     constexpr int B = decltype(bsel)::value;
+    constexpr bool WP = decltype(wp_sel)::value;
+    constexpr bool FZ = decltype(fz_sel)::value;
     const bf16_t *tKn = B ? sK0 : sK1;   // K of step j + 1
-    const bf16_t *tV = B ? sV1 : sV0;    // V of step j
     const int *tW = (B ? sW1 : sW0) + grp * kStepKeys;
     f32x16 (&s)[kStepBlocks] = sacc[B];
     f32x16 (&sn)[kStepBlocks] = sacc[1 - B];
-    const int kbase = j < nstep ? step_base(j) : a.L;   // past the group's steps: idle (barriers only)
+    const int kbase = j < nstep ? step_base(j) : a.L;
     const bool act = kbase < a.L;
-    const bool act_n = j + 1 < nstep && step_base(j + 1) < a.L;
+    const bool act_n = FZ && j + 1 < nstep && step_base(j + 1) < a.L;
     const bool partial = tile_of(j) < npart;
-    if (j + 1 < nstep) load_w(j + 1);
-    if (j + 2 < nstep) load_k(j + 2, B ? sK1 : sK0);
-    if (j + 1 < nstep) load_v(j + 1, B ? sV0 : sV1);
-
     if (act) {
       if (partial) {
         // a real branch: if-converted, full tiles would pay for the masking
@@ -340,26 +385,18 @@ __global__ __launch_bounds__(256 * NG, 2) void attn_fwd_kernel(AttnArgs a, int k
         ps = probs(s, m_run == kNegInfF ? 0.f : m_run);
       }
       l_run += ps;
-      // O^T += V^T P^T; operand t = (16-key slice t / DB, output block t % DB),
-      // read one ahead. The wave issues at raised priority meanwhile, so the
-      // SIMD's other wave, usually in its softmax, yields it the issue slots
-      // (about 1 % on the step)
-      __builtin_amdgcn_s_setprio(1);
-      bf16x8 vcur = tro.operand(tV, 0, 0);
-#pragma unroll
-      for (int t = 0; t < 2 * kStepBlocks * DB; ++t) {
-        bf16x8 vnext;
-        if (t + 1 < 2 * kStepBlocks * DB) vnext = tro.operand(tV, ((t + 1) / DB) * 16, (t + 1) % DB);
-        __builtin_amdgcn_sched_barrier(0);
-        oacc[t % DB] = mfma32<E>(vcur, pb[t / DB], oacc[t % DB]);
-        __builtin_amdgcn_sched_barrier(0);
-        if (t + 1 < 2 * kStepBlocks * DB) vcur = vnext;
-      }
-      __builtin_amdgcn_s_setprio(0);
+      if constexpr (WP) pv(B ? sV1 : sV0);
     } else if (act_n) {
       scores(tKn, sn);
     }
-
+  };
+  // step j (parity B): loads, softmax and O^T update, one barrier
+  auto run_step = [&](auto bsel, int j) {
+    constexpr int B = decltype(bsel)::value;
+    if (j + 1 < nstep) load_w(j + 1);
+    if (j + 2 < nstep) load_k(j + 2, B ? sK1 : sK0);
+    if (j + 1 < nstep) load_v(j + 1, B ? sV0 : sV1);
+    fphase(bsel, std::true_type{}, std::true_type{}, j);
     if (j + 1 < nstep) {
       __builtin_amdgcn_s_waitcnt(0);   // this thread's direct loads have landed
       store_w(B ? sW0 : sW1);
@@ -375,13 +412,79 @@ __global__ __launch_bounds__(256 * NG, 2) void attn_fwd_kernel(AttnArgs a, int k
     if (nstep > 1) load_k(1, sK1);
     __builtin_amdgcn_s_waitcnt(0);
     store_w(sW0);
+    if (MODE == kFwdPair && nstep > 1) {
+      // the pair form loads the codes of step j + 2 in V(j): step 1's here
+      load_w(1);
+      __builtin_amdgcn_s_waitcnt(0);
+      store_w(sW1);
+    }
   }
   __syncthreads();
   if (nstep > 0) scores(sK0, sacc[0]);   // step 0 always has keys
   __syncthreads();   // every wave is done with sK0 before step 0 loads into it
-  for (int j = 0; j < nloop; j += 2) {
-    run_step(std::integral_constant<int, 0>{}, j);
-    if (j + 1 < nloop) run_step(std::integral_constant<int, 1>{}, j + 1);
+  if constexpr (MODE == kFwdPair) {
+    // Intervals of one barrier each. A step is a softmax interval V(j)
+    // (masking, probabilities, row sums: VALU work only) and a product
+    // interval M(j) (the O^T update of step j and the scores of step j + 1:
+    // MFMAs and their operand reads only). The first row block (waves 0-3)
+    // runs V(j) in interval 2j and M(j) in 2j + 1, the second (waves 4-7) one
+    // interval later, after a leading idle interval (the first block closes
+    // with a trailing one), so each SIMD holds one wave in V and one in M and
+    // the matrix core works under the other wave's softmax. Both blocks run
+    // this one loop body.
+    // Loads: the first block issues K of step j + 2 (into K(j)'s buffer, read
+    // last in the second block's M(j - 1), interval 2j) and V of step j + 1
+    // (into V(j - 1)'s buffer, read last there too) at the start of its M(j),
+    // interval 2j + 1, under its MFMAs, and waits for them at the end of its
+    // V(j + 1), interval 2j + 2; both are first read in interval 2j + 3. The
+    // second block loads the codes of step j + 2 at the start of its V(j),
+    // interval 2j + 1, and stores them at the end of its M(j), interval
+    // 2j + 2, into step j's buffer (read last in interval 2j + 1); they are
+    // first read in interval 2j + 4. The prologue stages the codes of steps 0
+    // and 1. Each block keeps a load's issue and its store or wait inside one
+    // loop body: a value carried across the loop's back edge was copied
+    // between registers right after the tile loads, and the copy waited for
+    // them. The tile-list positions are read before the loads are issued (a
+    // list refill waits for every load in flight).
+    const bool late = wave >= 4;
+    const int ltid = tid - 256;   // thread of the second block
+    auto step2 = [&](auto bsel, int j) __attribute__((always_inline)) {
+      constexpr int B = decltype(bsel)::value;
+      const int sb0 = j < nstep ? step_base(j) : a.L;
+      const int sb1 = j + 1 < nstep ? step_base(j + 1) : a.L;
+      const int sb2 = j + 2 < nstep ? step_base(j + 2) : a.L;
+      // V(j). The second block loads the codes of step j + 2 (stored at the
+      // end of its M(j)); the first block's tile loads of its M(j - 1) (K of
+      // step j + 1, V of step j) land by the end of it.
+      if (late && j + 2 < nstep && ltid < kStepKeys) wkey.load(a.code, sb2 + ltid, a.P, a.L);
+      fphase(bsel, std::false_type{}, std::false_type{}, j);
+      if (!late) __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      // M(j): the first block issues K of step j + 2 and V of step j + 1
+      if (!late) {
+        if (j + 2 < nstep) load_tile(sb2, B ? sK1 : sK0, kp, a.k_ss, dmaK);
+        if (j + 1 < nstep) load_tile(sb1, B ? sV0 : sV1, vp, a.v_ss, dmaV);
+      }
+      if (sb0 < a.L) pv(B ? sV1 : sV0);                      // O^T += V^T P^T of step j
+      if (sb1 < a.L) scores(B ? sK0 : sK1, sacc[1 - B]);     // S^T of step j + 1
+      if (late && j + 2 < nstep) {
+        __builtin_amdgcn_s_waitcnt(0);   // the codes of step j + 2, into step j's buffer
+        if (ltid < kStepKeys)
+          *reinterpret_cast<int *>(const_cast<char *>(lds_at(B ? sW1 : sW0, opaque_u32(ltid * 4u)))) = wkey.w();
+      }
+      __syncthreads();
+    };
+    if (late) __syncthreads();
+    for (int j = 0; j < nloop; j += 2) {
+      step2(std::integral_constant<int, 0>{}, j);
+      if (j + 1 < nloop) step2(std::integral_constant<int, 1>{}, j + 1);
+    }
+    if (!late) __syncthreads();
+  } else {
+    for (int j = 0; j < nloop; j += 2) {
+      run_step(std::integral_constant<int, 0>{}, j);
+      if (j + 1 < nloop) run_step(std::integral_constant<int, 1>{}, j + 1);
+    }
   }
 
   if constexpr (NG == 2) {
@@ -432,25 +535,26 @@ __global__ __launch_bounds__(256 * NG, 2) void attn_fwd_kernel(AttnArgs a, int k
 
 // explicit instantiations: clang otherwise drops some host launch stubs of
 // this template (the bf16 ones), leaving undefined symbols
-template __global__ void attn_fwd_kernel<128, bf16_t, 1>(AttnArgs, int, int);
-template __global__ void attn_fwd_kernel<64, bf16_t, 1>(AttnArgs, int, int);
-template __global__ void attn_fwd_kernel<128, f16_t, 1>(AttnArgs, int, int);
-template __global__ void attn_fwd_kernel<64, f16_t, 1>(AttnArgs, int, int);
-template __global__ void attn_fwd_kernel<128, bf16_t, 2>(AttnArgs, int, int);
-template __global__ void attn_fwd_kernel<64, bf16_t, 2>(AttnArgs, int, int);
-template __global__ void attn_fwd_kernel<128, f16_t, 2>(AttnArgs, int, int);
-template __global__ void attn_fwd_kernel<64, f16_t, 2>(AttnArgs, int, int);
+#define MGA_FWD_INST(HD, T)                                                     \
+  template __global__ void attn_fwd_kernel<HD, T, kFwd4>(AttnArgs, int, int);    \
+  template __global__ void attn_fwd_kernel<HD, T, kFwdPair>(AttnArgs, int, int); \
+  template __global__ void attn_fwd_kernel<HD, T, kFwdSplit>(AttnArgs, int, int);
+MGA_FWD_INST(128, bf16_t)
+MGA_FWD_INST(64, bf16_t)
+MGA_FWD_INST(128, f16_t)
+MGA_FWD_INST(64, f16_t)
+#undef MGA_FWD_INST
 
-// Items per XCD that the 4-wave launch runs (the rest go to the two-group
-// launch): each XCD takes a contiguous 1/8 of the items on its slots (2
-// four-wave workgroups per CU). When the last round would fill at most half
-// of them -- a half-empty round takes as long as a full one here, a lone
-// workgroup on a CU running no faster -- that round's items run as
-// two-group workgroups (one per CU, each item in about half the time).
-// Items of fewer than 16 tiles are not split.
-int fwd_split_point(int items, int L, int cus) {
+// Items per XCD that the first launch runs (the rest go to the split launch):
+// each XCD takes a contiguous 1/8 of the items on its m workgroup slots. When
+// the last round would fill at most half of them -- a half-empty round takes
+// as long as a full one here, a lone workgroup on a CU running no faster --
+// that round's items run split (one 8-wave workgroup per row block, each in
+// about half the time); when all items fill at most half a round, all of them
+// do. Items of fewer than 16 tiles are not split.
+int fwd_split_point(int items, int L, int m) {
   const int nmax = (items + 7) / 8;
-  const int m = 2 * (cus / 8 > 0 ? cus / 8 : 1);
+  if (m < 1) m = 1;
   if (L < 16 * kBlock) return nmax;
   if (nmax <= m / 2) return 0;
   const int r = nmax % m;
@@ -461,14 +565,20 @@ template <int HD, typename T>
 static void fwd_launch(const AttnArgs &a, hipStream_t st) {
   const int G = a.Hq / a.Hkv;
   const int HPW = heads_per_wg(G);
-  const int QR = 32 * (4 / HPW);
-  const int nqb = (a.S + QR - 1) / QR;
+  const int U = units_per_item(HPW);
+  const int QU = U * 32 * (4 / HPW);
+  const int nqb = (a.S + QU - 1) / QU;
   const int items = a.Hkv * (G / HPW) * nqb;
   const int nmax = (items + 7) / 8;
-  const int k1 = fwd_split_point(items, a.L, device_cu_count());
-  if (k1 > 0) hipLaunchKernelGGL((attn_fwd_kernel<HD, T, 1>), dim3(8 * k1), dim3(256), 0, st, a, 0, k1);
+  const int cx = device_cu_count() / 8;   // CUs per XCD
+  const int k1 = fwd_split_point(items, a.L, U == 2 ? cx : 2 * cx);
+  if (k1 > 0) {
+    if (U == 2) hipLaunchKernelGGL((attn_fwd_kernel<HD, T, kFwdPair>), dim3(8 * k1), dim3(512), 0, st, a, 0, k1);
+    else hipLaunchKernelGGL((attn_fwd_kernel<HD, T, kFwd4>), dim3(8 * k1), dim3(256), 0, st, a, 0, k1);
+  }
   if (k1 < nmax)
-    hipLaunchKernelGGL((attn_fwd_kernel<HD, T, 2>), dim3(8 * (nmax - k1)), dim3(512), 0, st, a, k1, nmax - k1);
+    hipLaunchKernelGGL((attn_fwd_kernel<HD, T, kFwdSplit>), dim3(8 * U * (nmax - k1)), dim3(512), 0, st, a, k1,
+                       nmax - k1);
 }
 
 template <int HD>
