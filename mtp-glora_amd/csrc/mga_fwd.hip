@@ -1,25 +1,31 @@
 // MTP block-masked GQA attention forward for gfx950.
 //
 // Work item = (kv head g, slice of the G query heads, block of query rows).
-// A workgroup of 4 waves holds 4 (query head, 32-row block) pairs of one kv
-// head: with G a multiple of 4 that is 4 heads x the same rows, so every K/V
-// tile staged in LDS feeds four heads. Each wave computes
+// A wave holds one (query head, 32-row block) pair of one kv head and
+// computes
 //   S^T = K Q^T  (v_mfma_f32_32x32x16_bf16 / _f16; lane = query column)
 // over 64-key steps, keeps the online-softmax state of its queries in the lane
 // (plus one exchange with the lane 32 away) and accumulates O^T += V^T P^T,
 // feeding the probabilities from registers straight into the B operand. V^T
-// comes from the row-major V tile through the LDS transpose read. 32 rows per
-// wave, 2 waves per SIMD. A last round of items that would leave half of an
-// XCD's workgroup slots empty runs as 8-wave workgroups instead: two 4-wave
-// groups split one item's tile list and merge through LDS (NG = 2).
-//
-// Software pipeline: the scores of step j + 1 are computed while the softmax
-// of step j runs, in one scheduling region whose MFMAs and VALU instructions
-// are interleaved (the matrix cores and the VALU work at the same time instead
-// of in turn); then O^T takes step j's probabilities. K therefore runs one step
-// ahead of V: at step j the K tile of step j + 1 and the V tile of step j are
-// in LDS while the K tile of step j + 2 and the V tile of step j + 1 load
-// straight into the two other named buffers (one barrier per step).
+// comes from the row-major V tile through the LDS transpose read. Each K/V
+// tile staged in LDS feeds every wave of the workgroup (with G a multiple of
+// 4: 4 heads x the same rows per 4 waves). 2 waves per SIMD. Three forms:
+// * pair (G even): 8 waves, two 4-wave row blocks per item. A step is a
+//   softmax interval (VALU work only) and a product interval (the O^T update
+//   and the next step's scores: MFMAs only), one barrier each; the second
+//   block runs one interval behind the first, so each SIMD holds one wave in
+//   its softmax and one issuing MFMAs (a SIMD overlaps one wave's VALU work
+//   with another's MFMAs far better than the two kinds within one wave).
+// * 4-wave (G odd): one row block per workgroup, two workgroups per CU; the
+//   scores of step j + 1 are computed while the softmax of step j runs, in
+//   one scheduling region whose MFMAs and VALU instructions are interleaved,
+//   then O^T takes step j's probabilities (one barrier per step).
+// * split: a last round of items that would leave half of an XCD's workgroup
+//   slots empty runs each row block as an 8-wave workgroup whose two 4-wave
+//   groups split the tile list (as in the 4-wave form) and merge through LDS.
+// K runs one step ahead of V: while the K tile of step j + 1 and the V tile of
+// step j are read, the K tile of step j + 2 and the V tile of step j + 1 load
+// straight into the two other named buffers.
 //
 // Softmax without a per-step row max: probabilities are exp2(s * c - m) with
 // m the row's running offset, and a step is accepted when every lane's partial
@@ -76,10 +82,11 @@ enum { kFwd4 = 0, kFwdPair = 1, kFwdSplit = 2 };
 // * kFwdPair (U = 2): 8 waves, one workgroup per CU; each staged K/V tile
 //   feeds all 8 waves (half the tile loads and LDS writes per MFMA of two
 //   4-wave workgroups sharing the CU). A step runs as two barrier intervals,
-//   the scores and softmax (F) and the O^T update (P), and the second row
-//   block (waves 4-7, each sharing a SIMD with one of waves 0-3) runs one
-//   interval behind the first: each SIMD holds one wave in its softmax while
-//   the other multiplies, instead of two waves held in the same phase.
+//   the softmax (V: VALU work only) and the products (M: the O^T update and
+//   the next step's scores), and the second row block (waves 4-7, each
+//   sharing a SIMD with one of waves 0-3) runs one interval behind the
+//   first: each SIMD holds one wave in its softmax while the other issues
+//   MFMAs, instead of two waves held in the same phase.
 // * kFwd4 (U = 1): 4 waves, two workgroups per CU.
 // * kFwdSplit: each row block of an item as an 8-wave workgroup whose two
 //   4-wave groups take the even and the odd entries of the tile list and
