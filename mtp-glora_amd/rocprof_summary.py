@@ -9,10 +9,9 @@
   writes a known number of bytes (the largest-grid dispatch of that kernel).
   Each kernel's figure is its last dispatch in the pass (the hot-path launch;
   set-up work such as the prefix fill runs before it); for a kernel whose one
-  call is several launches (the forward's 4-wave launch and its two-group
-  tail launch, the dQ pass's 8-wave pair launch and its two-group tail
-  launch: ``MULTI_LAUNCH``) it is the sum over the last run of consecutive
-  dispatches of that kernel.
+  call is several launches (the forward's and the dQ pass's 8-wave pair or
+  4-wave launch and their two-group tail launch: ``MULTI_LAUNCH``) it is
+  the sum over the last run of consecutive dispatches of that kernel.
 
 * ``mfma``: ``--pmc`` runs of ``bench.py --pmc-pass`` collecting SQ and GRBM
   counters (any number of runs, each its own CSV) turned into per-kernel
@@ -51,20 +50,17 @@ def kernel_base(name: str) -> str:
 # kernels whose one call may be several consecutive launches
 MULTI_LAUNCH = ("attn_fwd_kernel", "attn_bwd_dq_kernel")
 
-# the dQ pass's forms by its last template argument
-DQ_FORMS = {"0": "4-wave", "1": "8-wave pair", "2": "two-group"}
+# the forward's and the dQ pass's forms by their last template argument
+FORMS = {"0": "4-wave", "1": "8-wave pair", "2": "two-group"}
 
 
 def kernel_label(name: str) -> str:
-    """kernel_base, telling the forward's two-group form (template argument
-    NG = 2, last in its argument list) from the 4-wave one, and the dQ pass's
-    three forms apart."""
+    """kernel_base, telling the three forms of the forward and of the dQ pass
+    apart (their last template argument) where the name carries it."""
     k = kernel_base(name)
     last = re.search(r"Li(\d)EEEv", name) or re.search(r",\s*(\d)>\(", name)
-    if k == "attn_fwd_kernel":
-        return k + (" (two-group)" if last and last.group(1) == "2" else " (4-wave)")
-    if k == "attn_bwd_dq_kernel" and last and last.group(1) in DQ_FORMS:
-        return f"{k} ({DQ_FORMS[last.group(1)]})"
+    if k in MULTI_LAUNCH and last and last.group(1) in FORMS:
+        return f"{k} ({FORMS[last.group(1)]})"
     return k
 
 

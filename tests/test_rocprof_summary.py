@@ -73,7 +73,10 @@ def test_kernel_labels_tell_the_forward_forms_apart():
     assert rs.kernel_label("_ZN3mga15attn_fwd_kernelILi128EDF16bLi2EEEvNS_8AttnArgsEii") == \
         "attn_fwd_kernel (two-group)"
     assert rs.kernel_label("_ZN3mga15attn_fwd_kernelILi128EDF16bLi1EEEvNS_8AttnArgsEii") == \
+        "attn_fwd_kernel (8-wave pair)"
+    assert rs.kernel_label("_ZN3mga15attn_fwd_kernelILi64EDF16_Li0EEEvNS_8AttnArgsEii") == \
         "attn_fwd_kernel (4-wave)"
+    assert rs.kernel_label("attn_fwd_kernel") == "attn_fwd_kernel"
     assert rs.kernel_label("void mga::attn_fwd_kernel<128, __bf16, 2>(mga::AttnArgs, int, int)") == \
         "attn_fwd_kernel (two-group)"
     assert rs.kernel_label("_ZN3mga18attn_bwd_dq_kernelILi128EDF16bEEvNS_8AttnArgsE") == "attn_bwd_dq_kernel"
