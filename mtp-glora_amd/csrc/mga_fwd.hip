@@ -180,12 +180,9 @@ __global__ __launch_bounds__(MODE == kFwd4 ? 256 : 512, 2) void attn_fwd_kernel(
       for (int mb = 0; mb < DB; ++mb) tro.off[sx][mb] = opaque_u32(tro.off[sx][mb] + gofs);
   }
 
-  // (kFwdPair: waves 0-3 load only K, waves 4-7 only V, so each wave keeps
-  // the lane offsets of one tile kind: dmaV is dmaK, set up with V's stride)
-  BufDma<HD, kStepKeys, NWD> dmaK, dmaV_own;
-  dmaK.init(MODE == kFwdPair && wave_id() >= 4 ? a.v_ss : a.k_ss);
-  if constexpr (MODE != kFwdPair) dmaV_own.init(a.v_ss);
-  const BufDma<HD, kStepKeys, NWD> &dmaV = MODE == kFwdPair ? dmaK : dmaV_own;
+  BufDma<HD, kStepKeys, NWD> dmaK, dmaV;
+  dmaK.init(a.k_ss);
+  dmaV.init(a.v_ss);
   KeyCode wkey;
   // rows past L (the last tile's tail) arrive as zeros; a step that starts
   // past L (the second half of the last tile) is never computed: no loads

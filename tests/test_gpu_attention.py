@@ -215,6 +215,48 @@ def test_plain_key_tensor_gets_full_gradient(mga, dev):
     check("dv", f64(vf.grad)[0], dvn)
 
 
+@pytest.mark.parametrize("heads", [(8, 2), (6, 2)], ids=["G4", "G3"])
+def test_key_value_row_strides_differ(mga, dev, heads):
+    """K and V as views of wider buffers with different row and head strides
+    (the kernels stage each tile with its own tensor's stride); G = 4 takes
+    the forward's 8-wave pair form, G = 3 the 4-wave one. L = P + S is not a
+    multiple of 64, so the last step of the key list is partly past L."""
+    Hq, Hkv = heads
+    D, P = 128, 300
+    print(f"row strides differ Hq={Hq} Hkv={Hkv}", flush=True)
+    seq = chunk_layout(260, 24, 4, P, seed=11)
+    S = len(seq.gate)
+    L = P + S
+    q, k, v, kp, vp, do = qkv(S, P, Hq, Hkv, D, torch.bfloat16, dev, seed=11)
+    kbig = torch.zeros(1, Hkv, L, D + 64, dtype=torch.bfloat16, device=dev)
+    vbig = torch.zeros(1, Hkv, L, D + 192, dtype=torch.bfloat16, device=dev)
+    kf = kbig[..., :D]
+    vf = vbig[..., 64:64 + D]
+    kf.copy_(torch.cat([kp, k], dim=2))
+    vf.copy_(torch.cat([vp, v], dim=2))
+    assert kf.stride(2) != vf.stride(2) and kf.stride(1) != vf.stride(1)
+    kf.requires_grad_()
+    vf.requires_grad_()
+    q.requires_grad_()
+    bm = mga.build_mtp_block_mask(torch.tensor(seq.gate, device=dev)[None], P)
+    o, lse = mga.mtp_attention(q, kf, vf, bm, D ** -0.5)
+    o.backward(do)
+    torch.cuda.synchronize()
+    allowed = mo.mtp_mask_dense(seq.gate, P)
+    kn, vn = f64(kf.detach())[0], f64(vf.detach())[0]
+    on, lsen = mo.attention_fwd(f64(q)[0], kn, vn, allowed, D ** -0.5)
+    dqn, dkn, dvn = mo.attention_bwd(f64(q)[0], kn, vn, on, lsen, f64(do)[0].transpose(1, 0, 2), allowed,
+                                     D ** -0.5)
+    check("o", f64(o)[0].transpose(1, 0, 2), on)
+    got_lse = f64(lse)[0]
+    assert np.array_equal(np.isneginf(got_lse), np.isneginf(lsen))
+    fin = np.isfinite(lsen)
+    check("lse", got_lse[fin], lsen[fin])
+    check("dq", f64(q.grad)[0], dqn)
+    check("dk", f64(kf.grad)[0], dkn)
+    check("dv", f64(vf.grad)[0], dvn)
+
+
 def test_transformers_wrapper_contract(mga, dev):
     """Output [B, S, Hq, D] contiguous and LSE cast to the value dtype, as
     flex_attention_forward returns ([tf]integrations/flex_attention.py:346, 367)."""
