@@ -411,9 +411,13 @@ __global__ __launch_bounds__(MODE == kFwd4 ? 256 : 512, 2) void attn_fwd_kernel(
   // prologue: K and V of step 0, K of step 1; the scores of step 0
   if (nstep > 0) {
     load_w(0);
-    load_k(0, sK0);
-    load_v(0, sV0);
-    if (nstep > 1) load_k(1, sK1);
+    // (in the pair form waves w and w + 4 stage the same quarter of a tile:
+    // the first block alone loads)
+    if (MODE != kFwdPair || wave < 4) {
+      load_k(0, sK0);
+      load_v(0, sV0);
+      if (nstep > 1) load_k(1, sK1);
+    }
     __builtin_amdgcn_s_waitcnt(0);
     store_w(sW0);
     if (MODE == kFwdPair && nstep > 1) {
