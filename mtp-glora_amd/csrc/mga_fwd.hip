@@ -440,20 +440,21 @@ __global__ __launch_bounds__(MODE == kFwd4 ? 256 : 512, 2) void attn_fwd_kernel(
     // with a trailing one), so each SIMD holds one wave in V and one in M and
     // the matrix core works under the other wave's softmax. Both blocks run
     // this one loop body.
-    // Loads: the first block issues K of step j + 2 (into K(j)'s buffer, read
-    // last in the second block's M(j - 1), interval 2j) and V of step j + 1
-    // (into V(j - 1)'s buffer, read last there too) at the start of its M(j),
-    // interval 2j + 1, under its MFMAs, and waits for them at the end of its
-    // V(j + 1), interval 2j + 2; both are first read in interval 2j + 3. The
-    // second block loads the codes of step j + 2 at the start of its V(j),
-    // interval 2j + 1, and stores them at the end of its M(j), interval
-    // 2j + 2, into step j's buffer (read last in interval 2j + 1); they are
-    // first read in interval 2j + 4. The prologue stages the codes of steps 0
-    // and 1. Each block keeps a load's issue and its store or wait inside one
-    // loop body: a value carried across the loop's back edge was copied
-    // between registers right after the tile loads, and the copy waited for
-    // them. The tile-list positions are read before the loads are issued (a
-    // list refill waits for every load in flight).
+    // Loads: the second block issues K of step j + 2 (into K(j)'s buffer, read
+    // last in its own M(j - 1), interval 2j) with the codes of step j + 2 at
+    // the start of its V(j), interval 2j + 1, waits for both at the end of
+    // its M(j), interval 2j + 2, and then stores the codes into step j's
+    // buffer (read last in interval 2j + 1); K is first read in interval
+    // 2j + 3, the codes in 2j + 4. The first block issues V of step j + 1
+    // (into V(j - 1)'s buffer, read last in the second block's M(j - 1),
+    // interval 2j) at the start of its M(j), interval 2j + 1, under its
+    // MFMAs, and waits for it at the end of its V(j + 1), interval 2j + 2; it
+    // is first read in interval 2j + 3. The prologue stages the codes of
+    // steps 0 and 1. Each block keeps a load's issue and its store or wait
+    // inside one loop body: a value carried across the loop's back edge was
+    // copied between registers right after the tile loads, and the copy
+    // waited for them. The tile-list positions are read before the loads are
+    // issued (a list refill waits for every load in flight).
     const bool late = wave >= 4;
     const int ltid = tid - 256;   // thread of the second block
     auto step2 = [&](auto bsel, int j) __attribute__((always_inline)) {
@@ -461,22 +462,24 @@ __global__ __launch_bounds__(MODE == kFwd4 ? 256 : 512, 2) void attn_fwd_kernel(
       const int sb0 = j < nstep ? step_base(j) : a.L;
       const int sb1 = j + 1 < nstep ? step_base(j + 1) : a.L;
       const int sb2 = j + 2 < nstep ? step_base(j + 2) : a.L;
-      // V(j). The second block loads the codes of step j + 2 (stored at the
-      // end of its M(j)); the first block's tile loads of its M(j - 1) (K of
-      // step j + 1, V of step j) land by the end of it.
-      if (late && j + 2 < nstep && ltid < kStepKeys) wkey.load(a.code, sb2 + ltid, a.P, a.L);
+      // V(j). The second block loads the codes and the K tile of step j + 2
+      // (the codes first: the compiler waits for every load in flight before
+      // it writes their register), stored or waited for at the end of its
+      // M(j); the first block's V load of its M(j - 1) (V of step j) lands by
+      // the end of it.
+      if (late && j + 2 < nstep) {
+        if (ltid < kStepKeys) wkey.load(a.code, sb2 + ltid, a.P, a.L);
+        load_tile(sb2, B ? sK1 : sK0, kp, a.k_ss, dmaK);
+      }
       fphase(bsel, std::false_type{}, std::false_type{}, j);
       if (!late) __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
-      // M(j): the first block issues K of step j + 2 and V of step j + 1
-      if (!late) {
-        if (j + 2 < nstep) load_tile(sb2, B ? sK1 : sK0, kp, a.k_ss, dmaK);
-        if (j + 1 < nstep) load_tile(sb1, B ? sV0 : sV1, vp, a.v_ss, dmaV);
-      }
+      // M(j): the first block issues V of step j + 1
+      if (!late && j + 1 < nstep) load_tile(sb1, B ? sV0 : sV1, vp, a.v_ss, dmaV);
       if (sb0 < a.L) pv(B ? sV1 : sV0);                      // O^T += V^T P^T of step j
       if (sb1 < a.L) scores(B ? sK0 : sK1, sacc[1 - B]);     // S^T of step j + 1
       if (late && j + 2 < nstep) {
-        __builtin_amdgcn_s_waitcnt(0);   // the codes of step j + 2, into step j's buffer
+        __builtin_amdgcn_s_waitcnt(0);   // K and the codes of step j + 2 (codes into step j's buffer)
         if (ltid < kStepKeys)
           *reinterpret_cast<int *>(const_cast<char *>(lds_at(B ? sW1 : sW0, opaque_u32(ltid * 4u)))) = wkey.w();
       }
