@@ -215,21 +215,24 @@ def test_plain_key_tensor_gets_full_gradient(mga, dev):
     check("dv", f64(vf.grad)[0], dvn)
 
 
-@pytest.mark.parametrize("heads", [(8, 2), (6, 2)], ids=["G4", "G3"])
-def test_key_value_row_strides_differ(mga, dev, heads):
+@pytest.mark.parametrize("heads,D,dtype", [((8, 2), 128, torch.bfloat16), ((6, 2), 128, torch.bfloat16),
+                                            ((8, 2), 64, torch.bfloat16), ((4, 2), 128, torch.float16)],
+                         ids=["G4", "G3", "G4-d64", "G2-fp16"])
+def test_key_value_row_strides_differ(mga, dev, heads, D, dtype):
     """K and V as views of wider buffers with different row and head strides
-    (the kernels stage each tile with its own tensor's stride); G = 4 takes
-    the forward's 8-wave pair form, G = 3 the 4-wave one. L = P + S is not a
-    multiple of 64, so the last step of the key list is partly past L."""
+    (the kernels stage each tile with its own tensor's stride); G = 4 and
+    G = 2 take the forward's 8-wave pair form, G = 3 the 4-wave one. L = P + S
+    is not a multiple of 64, so the last step of the key list is partly past
+    L."""
     Hq, Hkv = heads
-    D, P = 128, 300
-    print(f"row strides differ Hq={Hq} Hkv={Hkv}", flush=True)
+    P = 300
+    print(f"row strides differ Hq={Hq} Hkv={Hkv} D={D} {dtype}", flush=True)
     seq = chunk_layout(260, 24, 4, P, seed=11)
     S = len(seq.gate)
     L = P + S
-    q, k, v, kp, vp, do = qkv(S, P, Hq, Hkv, D, torch.bfloat16, dev, seed=11)
-    kbig = torch.zeros(1, Hkv, L, D + 64, dtype=torch.bfloat16, device=dev)
-    vbig = torch.zeros(1, Hkv, L, D + 192, dtype=torch.bfloat16, device=dev)
+    q, k, v, kp, vp, do = qkv(S, P, Hq, Hkv, D, dtype, dev, seed=11)
+    kbig = torch.zeros(1, Hkv, L, D + 64, dtype=dtype, device=dev)
+    vbig = torch.zeros(1, Hkv, L, D + 192, dtype=dtype, device=dev)
     kf = kbig[..., :D]
     vf = vbig[..., 64:64 + D]
     kf.copy_(torch.cat([kp, k], dim=2))
@@ -247,14 +250,17 @@ def test_key_value_row_strides_differ(mga, dev, heads):
     on, lsen = mo.attention_fwd(f64(q)[0], kn, vn, allowed, D ** -0.5)
     dqn, dkn, dvn = mo.attention_bwd(f64(q)[0], kn, vn, on, lsen, f64(do)[0].transpose(1, 0, 2), allowed,
                                      D ** -0.5)
-    check("o", f64(o)[0].transpose(1, 0, 2), on)
+    tol = (dict(max_abs=F16_MAX_ABS, mean_abs=F16_MEAN_ABS) if dtype == torch.float16
+           else dict(max_abs=MAX_ABS, mean_abs=MEAN_ABS))
+    check("o", f64(o)[0].transpose(1, 0, 2), on, **tol)
     got_lse = f64(lse)[0]
     assert np.array_equal(np.isneginf(got_lse), np.isneginf(lsen))
     fin = np.isfinite(lsen)
-    check("lse", got_lse[fin], lsen[fin])
-    check("dq", f64(q.grad)[0], dqn)
-    check("dk", f64(kf.grad)[0], dkn)
-    check("dv", f64(vf.grad)[0], dvn)
+    check("lse", got_lse[fin], lsen[fin], **tol)
+    scaled = dtype == torch.float16   # fp16 gradients: max bound relative above magnitude 1
+    check("dq", f64(q.grad)[0], dqn, **tol, scale_above_one=scaled)
+    check("dk", f64(kf.grad)[0], dkn, **tol, scale_above_one=scaled)
+    check("dv", f64(vf.grad)[0], dvn, **tol, scale_above_one=scaled)
 
 
 def test_transformers_wrapper_contract(mga, dev):
