@@ -758,7 +758,8 @@ def main() -> int:
     ap.add_argument("--north-star-steps", type=int, default=10,
                     help="timed steps of the north-star point (0 = skip)")
     ap.add_argument("--north-star-only", action="store_true",
-                    help="time the north-star point alone (for a kernel trace of that workload)")
+                    help="time the north-star point alone (for a kernel trace of that workload); with "
+                         "--pmc-pass, run the counter pass at that point")
     ap.add_argument("--extra", type=int, default=1,
                     help="also time the config-3 stream (36 layers x 8 chunks) and the config-5 step (0 = skip)")
     args = ap.parse_args()
@@ -784,11 +785,12 @@ def main() -> int:
 
     if args.config in STREAMS:
         return stream_bench(torch, mga, syn, args.config, STREAMS[args.config], args.cpu_reps)
-    if args.north_star_only:
+    if args.north_star_only and not args.pmc_pass:
         print(json.dumps({"north_star": north_star_phase(torch, mga, syn, max(args.north_star_steps, 1), 3)}))
         return 0
 
-    cfg = CONFIGS[args.config]
+    # (--pmc-pass --north-star-only: the counter pass at the north-star point)
+    cfg = NORTH_STAR if args.north_star_only else CONFIGS[args.config]
     Hq, Hkv, D, P = cfg["Hq"], cfg["Hkv"], cfg["D"], cfg["P"]
     n_reg = cfg["n_reg"]
     if cfg["every"]:
